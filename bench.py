@@ -1,0 +1,257 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused selective-scan training step on one MI355X.
+
+Default workload (the Mamba-130M layer shape): fp16
+storage / fp32 compute, B=8, L=2048, D=1536, N=16; one step = fused forward
+(checkpoint level 0) + fused backward through the drop-in autograd API, with
+all inputs resident in HBM. Prints ONE JSON line.
+
+  python bench.py [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4a|cfg4b]
+                  [--level 0|1] [--skip-cpu]
+
+`value` = B*L*D / ms_per_step (elements/s). `roofline` covers the dominant
+kernel (the fused backward call), timed live with HIP events on the stream
+the kernels run on; its algorithmic bytes are s*(5BLD + 4BLN + 2DN + 2D).
+`cpu_baseline` times the plain-PyTorch sequential restatement of the
+reference's CPU path (selective_scan_ref forward + autograd backward) on a
+bounded sample of the same workload on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "mamba-windows-cuda_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E peak
+METRIC = "fwd+bwd elements/sec (B·L·D) and achieved HBM GB/s vs peak, 1×MI355X"
+
+
+def _traffic_from_profiles(name):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
+    copy-kernel calibrated), read from the committed summary if present."""
+    path = os.path.join(ROOT, "profiles", f"{name}_pmc.txt")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read(), re.M)
+    return float(m.group(1)) if m else None
+
+
+def _events_ms(fn, n):
+    import torch
+
+    st = torch.cuda.current_stream()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    for _ in range(n):
+        fn()
+    b.record(st)
+    b.synchronize()
+    return a.elapsed_time(b) / n
+
+
+def bench_ssm(cfg, steps, warmup, level):
+    import torch
+
+    from mamba_windows_cuda import SelectiveScanCuda, ops, workloads
+
+    c = workloads.CONFIGS[cfg]
+    B, L, D = c["B"], c["L"], c["D"]
+    dtype = c["dtype"]
+    x = workloads.config_inputs(cfg, device="cuda", gen_device="cuda")
+    leaves = {k: x[k].requires_grad_(True) for k in ("u", "delta", "A", "B", "C", "D")}
+    dout = x["dout"]
+    m = SelectiveScanCuda(checkpoint_lvl=level)
+
+    def step():
+        for t in leaves.values():
+            t.grad = None
+        out = m(leaves["u"], leaves["delta"], leaves["A"], leaves["B"], leaves["C"], leaves["D"])
+        torch.autograd.backward(out, dout)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ms_events = _events_ms(step, steps)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    ms = max(ms_events, 0.0)
+
+    # live per-call timing of the fused kernels on the same stream
+    with torch.no_grad():
+        xs = {k: v.detach() for k, v in x.items()}
+        _, _, ckpt = ops.ssm_forward(xs["u"], xs["delta"], xs["A"], xs["B"], xs["C"], xs["D"], want_ckpt=True)
+        fwd = lambda: ops.ssm_forward(xs["u"], xs["delta"], xs["A"], xs["B"], xs["C"], xs["D"], want_ckpt=True,
+                                      want_h_last=False)
+        bwd = lambda: ops.ssm_backward(xs["u"], xs["delta"], xs["A"], xs["B"], xs["C"], xs["D"], dout, ckpt)
+        for _ in range(3):
+            fwd()
+            bwd()
+        n_k = max(steps, 10)
+        fwd_ms = _events_ms(fwd, n_k)
+        bwd_ms = _events_ms(bwd, n_k)
+
+    s = 2 if dtype == torch.float16 else 4
+    bytes_fwd = workloads.algorithmic_bytes(B, L, D, s, fwd=True, bwd=False)
+    bytes_bwd = workloads.algorithmic_bytes(B, L, D, s, fwd=False, bwd=True)
+    elems = B * L * D
+    gbs_bwd = bytes_bwd / (bwd_ms * 1e-3) / 1e9
+    gbs_step = (bytes_fwd + bytes_bwd) / (ms * 1e-3) / 1e9
+    res = {
+        "metric": METRIC,
+        "value": elems / (ms * 1e-3),
+        "unit": "elements/s",
+        "ms_per_step": ms,
+        "dtype": "f32",
+        "storage_dtype": "f16" if s == 2 else "f32",
+        "config": {"workload": f"{cfg}: selective scan fwd+bwd (fused), B={B} L={L} D={D} N=16, "
+                               f"checkpoint_lvl={level}", "B": B, "L": L, "D": D, "N": 16,
+                   "checkpoint_lvl": level},
+        "roofline": {"bound": "hbm", "kernel": "ssm_bwd (fused backward call)",
+                     "achieved": gbs_bwd, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": gbs_bwd / HBM_PEAK_GBS, "traffic": _traffic_from_profiles(f"ssm_bwd_{cfg}"),
+                     "algorithmic_bytes_per_launch": bytes_bwd, "avg_launch_ms": bwd_ms},
+        "kernels": {"ssm_fwd_ms": fwd_ms, "ssm_bwd_ms": bwd_ms,
+                    "fwd_algorithmic_GBps": bytes_fwd / (fwd_ms * 1e-3) / 1e9},
+        "step_hbm": {"algorithmic_bytes": bytes_fwd + bytes_bwd, "achieved_GBps": gbs_step,
+                     "frac_of_peak": gbs_step / HBM_PEAK_GBS},
+        "wall_ms_per_step": wall_ms,
+    }
+    return res
+
+
+def bench_pscan(steps, warmup):
+    import torch
+
+    from mamba_windows_cuda import parallel_scan_fn, workloads
+
+    a, b = workloads.pscan_inputs(device="cuda", gen_device="cuda")
+    for _ in range(warmup):
+        parallel_scan_fn(a, b)
+    torch.cuda.synchronize()
+    ms = _events_ms(lambda: parallel_scan_fn(a, b), steps)
+    nbytes = 3 * 4 * a.numel()
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {
+        "metric": "parallel_scan_fn elements/s and achieved HBM GB/s vs peak, 1×MI355X",
+        "value": a.numel() / (ms * 1e-3), "unit": "elements/s", "ms_per_step": ms, "dtype": "f32",
+        "config": {"workload": "cfg4b: parallel_scan_fn over (4, 65536, 1024) fp32", "shape": list(a.shape)},
+        "roofline": {"bound": "hbm", "kernel": "pscan (decoupled look-back)", "achieved": gbs,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
+                     "traffic": _traffic_from_profiles("pscan_cfg4b"), "algorithmic_bytes_per_launch": nbytes,
+                     "avg_launch_ms": ms},
+    }
+
+
+def bench_stream(steps, warmup):
+    """cfg4a: L=131072 fp32 fed as 32 chunks of 4096 through forward_with_state (no grad)."""
+    import torch
+
+    from mamba_windows_cuda import SelectiveScanCuda, workloads
+
+    x = workloads.config_inputs("cfg4a", device="cuda", gen_device="cuda", dout=False)
+    m = SelectiveScanCuda()
+
+    def run():
+        h = None
+        with torch.no_grad():
+            for s0 in range(0, 131072, 4096):
+                sl = slice(s0, s0 + 4096)
+                _, h = m.forward_with_state(x["u"][:, sl], x["delta"][:, sl], x["A"], x["B"][:, sl],
+                                            x["C"][:, sl], x["D"], h)
+        return h
+
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    ms = _events_ms(run, steps)
+    from mamba_windows_cuda.workloads import algorithmic_bytes
+
+    nbytes = algorithmic_bytes(1, 131072, 2048, 4, fwd=True, bwd=False) + 32 * 4 * 2 * 2048 * 16
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {
+        "metric": "streaming forward elements/s and achieved HBM GB/s vs peak, 1×MI355X",
+        "value": 131072 * 2048 / (ms * 1e-3), "unit": "elements/s", "ms_per_step": ms, "dtype": "f32",
+        "config": {"workload": "cfg4a: fp32 B=1 L=131072 D=2048 as 32 x 4096 chunks via forward_with_state"},
+        "roofline": {"bound": "hbm", "kernel": "ssm_fwd", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": gbs / HBM_PEAK_GBS, "traffic": None, "algorithmic_bytes_per_launch": nbytes / 32,
+                     "avg_launch_ms": ms / 32},
+    }
+
+
+def cpu_baseline(cfg, d_frac=2):
+    """Plain-PyTorch restatement of the reference's CPU path, structured like
+    selective_scan_ref (mamba_cuda.py:875-946: (B,D,N,L) dA/dBu then a loop
+    over L) with torch autograd for the backward, fp32, timed on a bounded
+    sample of the workload: batch row 0, full L, the first D/d_frac channels."""
+    import torch
+
+    from mamba_windows_cuda import workloads
+    from oracle import torch_ref
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    c = workloads.CONFIGS[cfg]
+    L, D = c["L"], c["D"] // d_frac
+    x = workloads.ssm_inputs(1, L, D, dtype=torch.float32, a_lo=c["a_lo"], a_hi=c["a_hi"], d_mode=c["d_mode"])
+
+    def once(n):
+        leaves = [x[k][:, :n].clone().requires_grad_(True) if x[k].dim() == 3 else x[k].clone().requires_grad_(True)
+                  for k in ("u", "delta", "A", "B", "C", "D")]
+        out, _ = torch_ref.selective_scan_vectorized(*leaves)
+        out.backward(x["dout"][:, :n])
+
+    once(16)  # load the CPU kernels
+    t = time.perf_counter()
+    once(L)
+    per = time.perf_counter() - t
+    return {"value": L * D / per, "unit": "elements/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{cfg} batch row 0, L={L}, first {D} of {c['D']} channels, fp32, forward + autograd "
+                      f"backward of the selective_scan_ref-structured restatement, 1 timed run of {per:.1f} s; "
+                      f"os.cpu_count()={os.cpu_count()}, affinity={cores}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="cfg2", choices=["cfg2", "cfg3", "cfg4a", "cfg4b"])
+    ap.add_argument("--level", type=int, default=0, choices=[0, 1])
+    ap.add_argument("--skip-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build measures one GPU only; multi-GPU sharding is design-only "
+                                   "(see DESIGN.md), run with --gpus 1"}))
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no HIP device visible"}))
+        sys.exit(1)
+    if args.config == "cfg4b":
+        res = bench_pscan(args.steps, args.warmup)
+    elif args.config == "cfg4a":
+        res = bench_stream(args.steps, args.warmup)
+    else:
+        res = bench_ssm(args.config, args.steps, args.warmup, args.level)
+        res["peak_hbm_allocated_GB"] = torch.cuda.max_memory_allocated() / 1e9
+    res.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+                "scaling": "weak", "vs_baseline": None, "data": "synthetic (seeded; BASELINE.json distributions)",
+                "device": torch.cuda.get_device_name(0)})
+    if not args.skip_cpu and args.config in ("cfg2", "cfg3"):
+        res["cpu_baseline"] = cpu_baseline(args.config)
+    print(json.dumps(res))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,77 @@
+"""ctypes binding of libmwc_ssm.so, the gfx950 C-ABI library (include/mwc_ssm.h).
+
+This replaces the reference's JIT bootstrap (``_get_selective_scan_cuda_module``,
+mamba_windows_cuda/mamba_cuda.py:832-872; ``_get_fused_module``,
+selective_scan_cuda_ext.py:530-559): the library is built ahead of time with
+hipcc for gfx950 and only loaded here. If it is missing the import of the
+operators fails loudly -- there is no CPU or PyTorch fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.environ.get("MWC_SSM_LIB", os.path.join(_HERE, "libmwc_ssm.so"))
+
+MWC_DTYPE_F32 = 0
+MWC_DTYPE_F16 = 1
+MWC_OK = 0
+CKPT_STEPS = 16  # MWC_CKPT_STEPS
+
+_lock = threading.Lock()
+_lib = None
+
+P = ctypes.c_void_p
+I64 = ctypes.c_int64
+SZ = ctypes.c_size_t
+
+_SIGNATURES = {
+    "mwc_abi_version": ([], ctypes.c_int),
+    "mwc_status_string": ([ctypes.c_int], ctypes.c_char_p),
+    "mwc_last_error": ([], ctypes.c_char_p),
+    "mwc_ssm_ckpt_count": ([I64], I64),
+    "mwc_ssm_fwd_workspace_size": ([I64, I64, I64, I64], SZ),
+    "mwc_ssm_fwd": ([ctypes.c_int, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, P, SZ, P], ctypes.c_int),
+    "mwc_ssm_bwd_workspace_size": ([I64, I64, I64, I64], SZ),
+    "mwc_ssm_bwd": ([ctypes.c_int, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, P, SZ, P],
+                    ctypes.c_int),
+    "mwc_pscan_workspace_size": ([I64, I64, I64], SZ),
+    "mwc_pscan_fwd": ([ctypes.c_int, P, P, P, I64, I64, I64, P, SZ, P], ctypes.c_int),
+    "mwc_pscan_bwd": ([ctypes.c_int, P, P, P, P, P, I64, I64, I64, P, SZ, P], ctypes.c_int),
+}
+
+EXPORTED = tuple(_SIGNATURES)
+
+
+class NativeLibraryMissing(ImportError):
+    pass
+
+
+def lib():
+    """Load (once) and return the native library; raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise NativeLibraryMissing(
+                    f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'` "
+                    "or `make -C mamba-windows-cuda_amd/csrc` (hipcc, gfx950)")
+            handle = ctypes.CDLL(LIB_PATH)
+            for name, (args, res) in _SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.argtypes = args
+                fn.restype = res
+            _lib = handle
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    """Raise RuntimeError (the reference's TORCH_CHECK surface) on a non-OK status."""
+    if status != MWC_OK:
+        L = lib()
+        msg = L.mwc_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what}: {L.mwc_status_string(status).decode()}: {msg}")

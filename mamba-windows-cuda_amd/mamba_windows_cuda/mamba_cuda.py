@@ -1,0 +1,149 @@
+"""Selective scan (Mamba-1, N=16) on MI355X -- the drop-in for
+``mamba_windows_cuda.mamba_cuda`` of zouyuanqing/mamba-windows-cuda.
+
+Same public names, signatures, shapes and dtype rules as the reference
+(mamba_windows_cuda/mamba_cuda.py:1044-1219); the work runs in the gfx950
+kernels of libmwc_ssm.so through the C ABI (see ops.py). Differences from the
+reference, all in the direction of correctness:
+
+* one fused forward and one fused backward serve every mode. The stateful
+  path no longer runs a Python loop over L in the forward (reference 1065-1068)
+  or the backward (987-1025), and its gradients are the true adjoint (the
+  reference's hand-written backward, 949-1041, mis-scales dA and ddelta);
+* h_prev/h_last are honoured by the backward as well (the reference's CUDA
+  backward kernels start from h = 0), giving dh_prev when h_prev is given;
+* nothing is saved for backward when no input requires grad.
+
+Checkpoint levels (the memory/speed knob of FusedSelectiveScan,
+selective_scan_cuda_ext.py:573-621, also accepted by SelectiveScanCuda):
+0 = the forward stores the fp32 state every 16 steps (B*ceil(L/16)*D*16*4
+bytes) and the backward restarts from it; 1 = only the inputs are kept and
+the backward first re-runs a state-only forward pass to rebuild them.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import ops
+
+
+def _forward_impl(ctx, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, checkpoint_lvl):
+    if checkpoint_lvl not in (0, 1):
+        raise RuntimeError(f"checkpoint_lvl must be 0 or 1 (got {checkpoint_lvl})")
+    n_in = 7 if h_prev is not None else 6
+    need_grad = any(ctx.needs_input_grad[:n_in])
+    out, h_last, ckpt = ops.ssm_forward(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev,
+                                        want_ckpt=need_grad and checkpoint_lvl == 0)
+    ctx.has_h_prev = h_prev is not None
+    ctx.need_grad = need_grad
+    if need_grad:
+        ctx.save_for_backward(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, ckpt)
+    ctx.set_materialize_grads(False)
+    return out, h_last
+
+
+def _backward_impl(ctx, dout, dh_last):
+    u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, ckpt = ctx.saved_tensors
+    if ckpt is None:  # recompute level: rebuild the state checkpoints
+        _, _, ckpt = ops.ssm_forward(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, want_out=False,
+                                     want_h_last=False, want_ckpt=True)
+    if dout is None:
+        dout = torch.zeros_like(u)
+    want_dh_prev = ctx.has_h_prev and ctx.needs_input_grad[6]
+    du, ddelta, dA, dB, dC, dD, dh_prev = ops.ssm_backward(u, delta, A, B_ssm, C_ssm, D_ssm, dout, ckpt,
+                                                           dh_last, want_dh_prev=want_dh_prev)
+    return du, ddelta, dA, dB, dC, dD, dh_prev
+
+
+class SelectiveScanCudaFunction(torch.autograd.Function):
+    """(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None) -> (out, h_last);
+    backward returns dh_prev when h_prev is given (mamba_cuda.py:1044-1096)."""
+
+    @staticmethod
+    def forward(ctx, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, checkpoint_lvl=0):
+        return _forward_impl(ctx, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, checkpoint_lvl)
+
+    @staticmethod
+    def backward(ctx, dout, dh_last):
+        g = _backward_impl(ctx, dout, dh_last)
+        return (*g, None)
+
+
+class SelectiveScanFn(torch.autograd.Function):
+    """Recompute level (the reference's V1, mamba_cuda.py:1099-1133): saves only the inputs."""
+
+    @staticmethod
+    def forward(ctx, u, delta, A, B_ssm, C_ssm, D_ssm):
+        out, _ = _forward_impl(ctx, u, delta, A, B_ssm, C_ssm, D_ssm, None, 1)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        return _backward_impl(ctx, grad_out, None)[:6]
+
+
+class SelectiveScanFnV2(torch.autograd.Function):
+    """Save level (the reference's V2, mamba_cuda.py:1136-1169): the forward keeps state checkpoints."""
+
+    @staticmethod
+    def forward(ctx, u, delta, A, B_ssm, C_ssm, D_ssm):
+        out, _ = _forward_impl(ctx, u, delta, A, B_ssm, C_ssm, D_ssm, None, 0)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        return _backward_impl(ctx, grad_out, None)[:6]
+
+
+class SelectiveScanCuda(torch.nn.Module):
+    """Mamba selective scan on MI355X with autograd (mamba_cuda.py:1172-1219).
+
+    ``forward(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None) -> out`` and
+    ``forward_with_state(...) -> (out, h_last)``. Shapes: u, delta (B, L, D);
+    A (D, 16); B_ssm, C_ssm (B, L, 16); D_ssm (D,); h_prev, h_last (B, D, 16).
+    All tensors fp32 or all fp16, on the GPU; outputs and gradients take the
+    input dtype. ``checkpoint_lvl`` (keyword, default 0) picks the memory/speed
+    trade-off described in the module docstring.
+    """
+
+    def __init__(self, checkpoint_lvl: int = 0):
+        super().__init__()
+        self.checkpoint_lvl = checkpoint_lvl
+
+    def forward(self, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None):
+        out, _ = SelectiveScanCudaFunction.apply(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, self.checkpoint_lvl)
+        return out
+
+    def forward_with_state(self, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None):
+        """Returns (out (B, L, D), h_last (B, D, N)); h_last feeds the next chunk's h_prev."""
+        return SelectiveScanCudaFunction.apply(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, self.checkpoint_lvl)
+
+
+def selective_scan_ref(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, return_intermediates=False):
+    """Plain-PyTorch sequential selective scan (any device, autograd-capable),
+    the reference's ``selective_scan_ref`` API (mamba_cuda.py:875-946).
+
+    Returns (out (B,L,D), h_last (B,D,N)) and, with return_intermediates, a
+    dict of the (B,D,N,L) tensors 'h_states', 'dA', 'dBu' plus the transposed
+    inputs. Not used by the GPU path.
+    """
+    bsz, L, dm = u.shape
+    n = A.shape[1]
+    u_t, d_t = u.transpose(1, 2), delta.transpose(1, 2)
+    B_t, C_t = B_ssm.transpose(1, 2), C_ssm.transpose(1, 2)
+    if h_prev is None:
+        h_prev = torch.zeros(bsz, dm, n, device=u.device, dtype=u.dtype)
+    dA = torch.exp(d_t.unsqueeze(2) * A.unsqueeze(0).unsqueeze(-1))   # (B,D,N,L)
+    dBu = (d_t * u_t).unsqueeze(2) * B_t.unsqueeze(1)                # (B,D,N,L)
+    h = h_prev
+    states = []
+    for t in range(L):
+        h = dA[..., t] * h + dBu[..., t]
+        states.append(h)
+    h_states = torch.stack(states, dim=-1) if states else h_prev.new_zeros(bsz, dm, n, 0)
+    y = (C_t.unsqueeze(1) * h_states).sum(2) + u_t * D_ssm.view(1, -1, 1)
+    out = y.transpose(1, 2)
+    if return_intermediates:
+        return out, h, {"h_states": h_states, "dA": dA, "dBu": dBu, "u_t": u_t, "delta_t": d_t,
+                        "B_t": B_t, "C_t": C_t, "h_prev": h_prev}
+    return out, h

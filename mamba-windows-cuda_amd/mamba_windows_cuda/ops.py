@@ -1,0 +1,186 @@
+"""Validated host wrappers over the C ABI (one call = one enqueue on the
+current HIP stream). Tensors are borrowed; outputs and scratch come from the
+torch caching allocator.
+
+The validation restates the reference host wrapper's contract and messages
+(``selective_scan_cuda_forward_with_state``, mamba_windows_cuda/mamba_cuda.py:
+281-326): device, dtype (fp32/fp16, all equal), last-dim contiguity, N == 16,
+ranks and shapes, then the optional h_prev. Violations raise RuntimeError
+before any device work is queued.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+NSTATE = 16
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    return _lib.MWC_DTYPE_F16 if t.dtype == torch.float16 else _lib.MWC_DTYPE_F32
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(dev: torch.device):
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def check_ssm_inputs(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, *, require_device=True):
+    """Raise RuntimeError unless the inputs satisfy the reference's contract."""
+    named = (("u", u), ("delta", delta), ("A", A), ("B_ssm", B_ssm), ("C_ssm", C_ssm), ("D_ssm", D_ssm))
+    if require_device:
+        for name, t in named:
+            _require(t.is_cuda, f"{name} must be a CUDA tensor")
+    _require(u.dtype in (torch.float32, torch.float16), "u must be float32/float16")
+    for name, t in named[1:]:
+        _require(t.dtype == u.dtype, f"{name} dtype must match u dtype")
+    for name, t in named:
+        _require(t.dim() == 0 or t.stride(-1) == 1 or t.size(-1) == 1,
+                 f"{name} must be contiguous in the last dimension")
+    _require(A.dim() == 2, "A must be 2D (dim, state)")
+    _require(A.size(1) == NSTATE, "Only N=16 is supported")
+    _require(u.dim() == 3, "u must be 3D (batch, seqlen, dim)")
+    _require(delta.dim() == 3, "delta must be 3D (batch, seqlen, dim)")
+    _require(B_ssm.dim() == 3, "B_ssm must be 3D (batch, seqlen, state)")
+    _require(C_ssm.dim() == 3, "C_ssm must be 3D (batch, seqlen, state)")
+    _require(D_ssm.dim() == 1, "D_ssm must be 1D (dim)")
+    bsz, L, dm = u.shape
+    _require(tuple(delta.shape) == (bsz, L, dm), "delta shape mismatch")
+    _require(tuple(A.shape) == (dm, NSTATE), "A shape mismatch")
+    _require(tuple(B_ssm.shape) == (bsz, L, NSTATE), "B_ssm shape mismatch")
+    _require(tuple(C_ssm.shape) == (bsz, L, NSTATE), "C_ssm shape mismatch")
+    _require(tuple(D_ssm.shape) == (dm,), "D_ssm shape mismatch")
+    devs = {t.device for _, t in named}
+    _require(len(devs) == 1, "all inputs must be on the same device")
+    if h_prev is not None:
+        if require_device:
+            _require(h_prev.is_cuda, "h_prev must be a CUDA tensor")
+        _require(h_prev.dtype == u.dtype, "h_prev dtype must match u dtype")
+        _require(h_prev.dim() == 0 or h_prev.stride(-1) == 1 or h_prev.size(-1) == 1,
+                 "h_prev must be contiguous in the last dimension")
+        _require(h_prev.dim() == 3, "h_prev must be 3D (batch, dim, state)")
+        _require(tuple(h_prev.shape) == (bsz, dm, NSTATE), "h_prev shape must be (B, D, N)")
+        _require(h_prev.device == u.device, "h_prev must be on the same device as u")
+
+
+def ckpt_count(seqlen: int) -> int:
+    return int(_lib.lib().mwc_ssm_ckpt_count(seqlen))
+
+
+def ssm_forward(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, *, want_out=True, want_h_last=True,
+                want_ckpt=False):
+    """Fused forward. Returns (out or None, h_last or None, ckpt or None).
+
+    ckpt is fp32 (B, ceil(L/16), D, 16): the state before every 16th step,
+    which the backward restarts from."""
+    check_ssm_inputs(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev)
+    u, delta, A, B_ssm, C_ssm, D_ssm = (t.contiguous() for t in (u, delta, A, B_ssm, C_ssm, D_ssm))
+    h_prev = None if h_prev is None else h_prev.contiguous()
+    L_ = _lib.lib()
+    bsz, L, dm = u.shape
+    dev = u.device
+    out = torch.empty_like(u) if want_out else None
+    h_last = torch.empty(bsz, dm, NSTATE, dtype=u.dtype, device=dev) if want_h_last else None
+    ckpt = (torch.empty(bsz, ckpt_count(L), dm, NSTATE, dtype=torch.float32, device=dev)
+            if want_ckpt else None)
+    nbytes = L_.mwc_ssm_fwd_workspace_size(bsz, L, dm, NSTATE)
+    ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        st = L_.mwc_ssm_fwd(_dtype_code(u), _ptr(u), _ptr(delta), _ptr(A), _ptr(B_ssm), _ptr(C_ssm), _ptr(D_ssm),
+                            _ptr(h_prev), _ptr(out), _ptr(h_last), _ptr(ckpt), bsz, L, dm, NSTATE,
+                            ws.data_ptr(), nbytes, _stream(dev))
+    _lib.check(st, "mwc_ssm_fwd")
+    return out, h_last, ckpt
+
+
+def ssm_backward(u, delta, A, B_ssm, C_ssm, D_ssm, dout, ckpt, dh_last=None, want_dh_prev=False):
+    """Fused backward. Returns (du, ddelta, dA, dB, dC, dD, dh_prev or None), in u's dtype."""
+    u, delta, A, B_ssm, C_ssm, D_ssm = (t.contiguous() for t in (u, delta, A, B_ssm, C_ssm, D_ssm))
+    bsz, L, dm = u.shape
+    dout = dout.to(u.dtype).contiguous()
+    _require(tuple(dout.shape) == (bsz, L, dm), "dout shape mismatch")
+    if dh_last is not None:
+        dh_last = dh_last.to(u.dtype).contiguous()
+        _require(tuple(dh_last.shape) == (bsz, dm, NSTATE), "dh_last shape must be (B, D, N)")
+    _require(ckpt is not None and ckpt.dtype == torch.float32 and ckpt.is_contiguous()
+             and tuple(ckpt.shape) == (bsz, ckpt_count(L), dm, NSTATE), "ckpt does not match the inputs")
+    L_ = _lib.lib()
+    dev = u.device
+    du = torch.empty_like(u)
+    ddelta = torch.empty_like(u)
+    dA = torch.empty_like(A)
+    dB = torch.empty_like(B_ssm)
+    dC = torch.empty_like(C_ssm)
+    dD = torch.empty_like(D_ssm)
+    dh_prev = torch.empty(bsz, dm, NSTATE, dtype=u.dtype, device=dev) if want_dh_prev else None
+    nbytes = L_.mwc_ssm_bwd_workspace_size(bsz, L, dm, NSTATE)
+    ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        st = L_.mwc_ssm_bwd(_dtype_code(u), _ptr(u), _ptr(delta), _ptr(A), _ptr(B_ssm), _ptr(C_ssm), _ptr(D_ssm),
+                            None, _ptr(dout), _ptr(dh_last), _ptr(ckpt), _ptr(du), _ptr(ddelta), _ptr(dA), _ptr(dB),
+                            _ptr(dC), _ptr(dD), _ptr(dh_prev), bsz, L, dm, NSTATE, ws.data_ptr(), nbytes,
+                            _stream(dev))
+    _lib.check(st, "mwc_ssm_bwd")
+    return du, ddelta, dA, dB, dC, dD, dh_prev
+
+
+def _scan_view(x: torch.Tensor):
+    """(B, D, L, N) -> (B*D, L, N) and (B, L, C) -> itself; the scan runs over dim -2."""
+    if x.dim() == 4:
+        b, d, l, n = x.shape
+        return x.reshape(b * d, l, n)
+    if x.dim() == 3:
+        return x
+    raise RuntimeError("parallel scan inputs must be 4D (B, D, L, N) or 3D (B, L, C)")
+
+
+def _check_scan(*ts):
+    for t in ts:
+        _require(t.is_cuda, "parallel_scan_fn inputs must be CUDA tensors")
+        _require(t.dtype in (torch.float32, torch.float16), "parallel_scan_fn supports float32/float16")
+        _require(t.dtype == ts[0].dtype and tuple(t.shape) == tuple(ts[0].shape),
+                 "parallel_scan_fn inputs must share dtype and shape")
+        _require(t.device == ts[0].device, "parallel_scan_fn inputs must share a device")
+
+
+def pscan_forward(A, X):
+    _check_scan(A, X)
+    A, X = A.contiguous(), X.contiguous()
+    a3, x3 = _scan_view(A), _scan_view(X)
+    H = torch.empty_like(X)
+    h3 = _scan_view(H)
+    nseq, L, nc = x3.shape
+    L_ = _lib.lib()
+    nbytes = L_.mwc_pscan_workspace_size(nseq, L, nc)
+    ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=X.device)
+    with torch.cuda.device(X.device):
+        st = L_.mwc_pscan_fwd(_dtype_code(X), a3.data_ptr(), x3.data_ptr(), h3.data_ptr(), nseq, L, nc,
+                              ws.data_ptr(), nbytes, _stream(X.device))
+    _lib.check(st, "mwc_pscan_fwd")
+    return H
+
+
+def pscan_backward(A, H, dH):
+    _check_scan(A, H, dH)
+    A, H, dH = A.contiguous(), H.contiguous(), dH.contiguous()
+    dA = torch.empty_like(A)
+    dX = torch.empty_like(A)
+    a3, h3, g3, da3, dx3 = (_scan_view(t) for t in (A, H, dH, dA, dX))
+    nseq, L, nc = h3.shape
+    L_ = _lib.lib()
+    nbytes = L_.mwc_pscan_workspace_size(nseq, L, nc)
+    ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=H.device)
+    with torch.cuda.device(H.device):
+        st = L_.mwc_pscan_bwd(_dtype_code(H), a3.data_ptr(), h3.data_ptr(), g3.data_ptr(), da3.data_ptr(),
+                              dx3.data_ptr(), nseq, L, nc, ws.data_ptr(), nbytes, _stream(H.device))
+    _lib.check(st, "mwc_pscan_bwd")
+    return dA, dX

@@ -1,0 +1,141 @@
+"""CPU-only checks of the C-ABI library and the host layer (no kernel launches)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mwc_ssm.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(mwc_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from mamba_windows_cuda import _lib
+
+    L = _lib.lib()
+    names = _declared()
+    assert len(names) >= 11
+    for n in names:
+        assert hasattr(L, n), n
+    assert set(names) == set(_lib.EXPORTED)
+    assert L.mwc_abi_version() == 1
+
+
+def test_status_strings_and_ckpt_count():
+    from mamba_windows_cuda import _lib
+
+    L = _lib.lib()
+    assert L.mwc_status_string(0) == b"MWC_OK"
+    assert L.mwc_status_string(1) == b"MWC_ERR_INVALID_ARGUMENT"
+    assert L.mwc_ssm_ckpt_count(0) == 0
+    assert L.mwc_ssm_ckpt_count(1) == 1
+    assert L.mwc_ssm_ckpt_count(16) == 1
+    assert L.mwc_ssm_ckpt_count(17) == 2
+    assert L.mwc_ssm_ckpt_count(2048) == 128
+
+
+def test_argument_errors_before_any_launch():
+    """Contract violations return a status before the library touches the device."""
+    from mamba_windows_cuda import _lib
+
+    L = _lib.lib()
+    fake = ctypes.c_void_p(16)
+    # N != 16 (mamba_cuda.py:215)
+    st = L.mwc_ssm_fwd(1, fake, fake, fake, fake, fake, fake, None, fake, None, None, 1, 8, 8, 15, fake, 1 << 20, None)
+    assert st == 1 and b"N=16" in L.mwc_last_error()
+    # bad dtype
+    st = L.mwc_ssm_fwd(7, fake, fake, fake, fake, fake, fake, None, fake, None, None, 1, 8, 8, 16, fake, 1 << 20, None)
+    assert st == 1
+    # workspace too small
+    st = L.mwc_ssm_fwd(0, fake, fake, fake, fake, fake, fake, None, fake, None, None, 1, 8, 8, 16, fake, 4, None)
+    assert st == 3 and b"workspace" in L.mwc_last_error()
+    # backward without checkpoints
+    st = L.mwc_ssm_bwd(0, fake, fake, fake, fake, fake, fake, None, fake, None, None, fake, fake, fake, fake, fake,
+                       fake, None, 1, 8, 8, 16, fake, 1 << 20, None)
+    assert st == 1
+    # scan: negative size, missing pointer
+    assert L.mwc_pscan_fwd(0, fake, fake, fake, -1, 8, 8, fake, 1 << 20, None) == 1
+    assert L.mwc_pscan_fwd(0, None, fake, fake, 1, 8, 8, fake, 1 << 20, None) == 1
+    # empty problems are no-ops
+    assert L.mwc_ssm_fwd(0, None, None, fake, None, None, fake, None, None, None, None, 0, 8, 8, 16, None, 0, None) == 0
+    assert L.mwc_pscan_fwd(0, None, None, None, 0, 8, 8, None, 0, None) == 0
+
+
+def test_workspace_sizes_monotone():
+    from mamba_windows_cuda import _lib
+
+    L = _lib.lib()
+    a = L.mwc_ssm_bwd_workspace_size(8, 2048, 1536, 16)
+    b = L.mwc_ssm_bwd_workspace_size(8, 4096, 1536, 16)
+    assert 0 < a < b
+    assert L.mwc_ssm_fwd_workspace_size(8, 2048, 1536, 16) == 8 * 2048 * 32 * 4
+    assert L.mwc_pscan_workspace_size(4, 65536, 1024) > 0
+
+
+def _valid(dtype=torch.float32, B=2, L=5, D=3):
+    return dict(u=torch.randn(B, L, D, dtype=dtype), delta=torch.rand(B, L, D, dtype=dtype),
+                A=-torch.rand(D, 16, dtype=dtype), B_ssm=torch.randn(B, L, 16, dtype=dtype),
+                C_ssm=torch.randn(B, L, 16, dtype=dtype), D_ssm=torch.ones(D, dtype=dtype))
+
+
+@pytest.mark.parametrize("mutate,msg", [
+    (lambda x: x.update(A=torch.randn(3, 15)), "Only N=16"),
+    (lambda x: x.update(u=x["u"].double()), "float32/float16"),
+    (lambda x: x.update(delta=x["delta"].half()), "delta dtype must match"),
+    (lambda x: x.update(u=x["u"][0]), "u must be 3D"),
+    (lambda x: x.update(B_ssm=torch.randn(2, 4, 16)), "B_ssm shape mismatch"),
+    (lambda x: x.update(D_ssm=torch.ones(4)), "D_ssm shape mismatch"),
+    (lambda x: x.update(C_ssm=torch.randn(2, 16, 5).transpose(1, 2)), "C_ssm must be contiguous"),
+    (lambda x: x.update(h_prev=torch.randn(2, 3, 17)), "h_prev shape must be"),
+    (lambda x: x.update(h_prev=torch.randn(3, 3, 16)), "h_prev shape must be"),
+    (lambda x: x.update(h_prev=torch.randn(2, 3, 16).half()), "h_prev dtype"),
+])
+def test_validation_contract(mutate, msg):
+    """Same failures as the reference's TORCH_CHECKs (mamba_cuda.py:281-326), as RuntimeError."""
+    from mamba_windows_cuda import ops
+
+    x = _valid()
+    mutate(x)
+    with pytest.raises(RuntimeError, match=msg):
+        ops.check_ssm_inputs(x["u"], x["delta"], x["A"], x["B_ssm"], x["C_ssm"], x["D_ssm"], x.get("h_prev"),
+                             require_device=False)
+
+
+def test_cpu_tensors_are_rejected_not_computed():
+    """No CPU fallback: host tensors raise like the reference's is_cuda checks."""
+    from mamba_windows_cuda import FusedSelectiveScan, SelectiveScanCuda, parallel_scan_fn
+
+    x = _valid()
+    with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
+        SelectiveScanCuda()(x["u"], x["delta"], x["A"], x["B_ssm"], x["C_ssm"], x["D_ssm"])
+    with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
+        FusedSelectiveScan(1).forward_with_state(x["u"], x["delta"], x["A"], x["B_ssm"], x["C_ssm"], x["D_ssm"])
+    with pytest.raises(RuntimeError, match="CUDA"):
+        parallel_scan_fn(torch.rand(1, 2, 8, 4), torch.rand(1, 2, 8, 4))
+
+
+def test_reference_api_functions_on_cpu():
+    """selective_scan_ref / parallel_scan_ref are plain-PyTorch API functions (any device)."""
+    import numpy as np
+
+    from mamba_windows_cuda import parallel_scan_ref, selective_scan_ref
+    from oracle import oracle as orc
+
+    x = _valid(B=2, L=9, D=4)
+    hp = torch.randn(2, 4, 16)
+    out, hl = selective_scan_ref(x["u"], x["delta"], x["A"], x["B_ssm"], x["C_ssm"], x["D_ssm"], hp)
+    ro, rh = orc.ssm_fwd(x["u"], x["delta"], x["A"], x["B_ssm"], x["C_ssm"], x["D_ssm"], hp)
+    np.testing.assert_allclose(out.numpy(), ro, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(hl.numpy(), rh, rtol=1e-4, atol=1e-5)
+    _, _, inter = selective_scan_ref(x["u"], x["delta"], x["A"], x["B_ssm"], x["C_ssm"], x["D_ssm"],
+                                     return_intermediates=True)
+    assert inter["h_states"].shape == (2, 4, 16, 9)
+    A = torch.rand(2, 3, 11, 5)
+    X = torch.randn(2, 3, 11, 5)
+    np.testing.assert_allclose(parallel_scan_ref(A, X).numpy(), orc.pscan_fwd(A, X), rtol=1e-5, atol=1e-6)

@@ -1,0 +1,199 @@
+"""GPU parity of the fused selective-scan kernels against the float64 oracle.
+
+Inputs are generated on the CPU (seeded), cast to the test dtype, and the
+oracle runs in float64 on exactly those dtype-rounded values. Tolerances
+(|x - y| <= atol + rtol*|y|): fp32 rtol 1e-3 / atol 1e-4, fp16 rtol 1e-2 /
+atol 1e-2, applied to out, h_last and every gradient.
+"""
+import numpy as np
+import pytest
+import torch
+
+from mamba_windows_cuda import FusedSelectiveScan, SelectiveScanCuda, workloads
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: dict(rtol=1e-3, atol=1e-4), torch.float16: dict(rtol=1e-2, atol=1e-2)}
+GRADS = (("u", "du"), ("delta", "ddelta"), ("A", "dA"), ("B", "dB"), ("C", "dC"), ("D", "dD"))
+
+
+def _np(t):
+    return t.detach().cpu().double().numpy()
+
+
+def _close(name, got, ref, dtype):
+    np.testing.assert_allclose(_np(got), ref, err_msg=name, **TOL[dtype])
+
+
+def _run(x, dev, *, with_h, dh_last=None, lvl=0, grads=True):
+    """forward_with_state + backward through the drop-in API; returns out, h_last, grads dict."""
+    leaves = {k: v.to(dev).requires_grad_(grads and k not in ("dout",)) for k, v in x.items()}
+    m = SelectiveScanCuda(checkpoint_lvl=lvl)
+    out, h_last = m.forward_with_state(leaves["u"], leaves["delta"], leaves["A"], leaves["B"], leaves["C"],
+                                       leaves["D"], leaves["h_prev"] if with_h else None)
+    g = {}
+    if grads:
+        loss = (out.float() * leaves["dout"].float()).sum()
+        if dh_last is not None:
+            loss = loss + (h_last.float() * dh_last.to(dev).float()).sum()
+        loss.backward()
+        g = {k: leaves[k].grad for k in leaves if leaves[k].grad is not None}
+    torch.cuda.synchronize()
+    return out, h_last, g
+
+
+# (B, L, D): lane-group widths 1/2/4 states per lane are chosen by B*D; ragged D and L on purpose.
+SHAPES = [(1, 77, 70), (2, 45, 1100), (4, 33, 2100), (3, 1, 20), (1, 16, 16), (2, 130, 64)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("with_h", [False, True])
+def test_forward_backward_parity(dev, shape, dtype, with_h):
+    B, L, D = shape
+    print(f"case fwd+bwd shape={shape} dtype={dtype} h_prev={with_h}", flush=True)
+    x = workloads.ssm_inputs(B, L, D, dtype=dtype, h_prev=True, seed=B * 1000 + L + D)
+    dhl = (0.5 * torch.randn(B, D, 16, generator=torch.Generator().manual_seed(3))).to(dtype) if with_h else None
+    out, h_last, g = _run(x, dev, with_h=with_h, dh_last=dhl)
+    hp = x["h_prev"] if with_h else None
+    ro, rh = orc.ssm_fwd(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], hp, clamp=True)
+    _close("out", out, ro, dtype)
+    _close("h_last", h_last, rh, dtype)
+    r = orc.ssm_bwd(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["dout"], hp, dhl, clamp=True)
+    for k, name in GRADS:
+        _close(name, g[k], r[name], dtype)
+    if with_h:
+        _close("dh_prev", g["h_prev"], r["dh_prev"], dtype)
+
+
+def test_checkpoint_levels_agree_bitwise(dev):
+    x = workloads.ssm_inputs(2, 300, 96, dtype=torch.float32, h_prev=True, seed=5)
+    _, _, g0 = _run(x, dev, with_h=True, lvl=0)
+    _, _, g1 = _run(x, dev, with_h=True, lvl=1)
+    for k in g0:
+        assert torch.equal(g0[k], g1[k]), k
+    f0 = FusedSelectiveScan(0).to(dev)
+    f1 = FusedSelectiveScan(1).to(dev)
+    xd = {k: v.to(dev) for k, v in x.items()}
+    o0 = f0(xd["u"], xd["delta"], xd["A"], xd["B"], xd["C"], xd["D"])
+    o1, _ = f1.forward_with_state(xd["u"], xd["delta"], xd["A"], xd["B"], xd["C"], xd["D"])
+    assert torch.equal(o0, o1)
+
+
+def test_repeatable(dev):
+    x = workloads.ssm_inputs(2, 200, 2100, dtype=torch.float16, seed=6)
+    o1, _, g1 = _run(x, dev, with_h=False)
+    o2, _, g2 = _run(x, dev, with_h=False)
+    assert torch.equal(o1, o2)
+    for k in g1:
+        assert torch.equal(g1[k], g2[k]), k
+
+
+def test_config0_forward(dev):
+    x = workloads.config_inputs("cfg0")
+    out, h_last, _ = _run(x, dev, with_h=False, grads=False)
+    ro, rh = orc.ssm_fwd(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], None, clamp=True)
+    _close("out", out, ro, torch.float32)
+    _close("h_last", h_last, rh, torch.float32)
+
+
+def test_config1_stateful_forward(dev):
+    x = workloads.config_inputs("cfg1")
+    out, h_last, _ = _run(x, dev, with_h=True, grads=False)
+    ro, rh = orc.ssm_fwd(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["h_prev"], clamp=True)
+    _close("out", out, ro, torch.float16)
+    _close("h_last", h_last, rh, torch.float16)
+
+
+def test_config2_training_step(dev):
+    """Mamba-130M layer shape, fp16: out and all six gradients vs the float64 oracle."""
+    x = workloads.config_inputs("cfg2")
+    out, _, g = _run(x, dev, with_h=False)
+    ro, _ = orc.ssm_fwd(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], None, clamp=True)
+    _close("out", out, ro, torch.float16)
+    del ro
+    r = orc.ssm_bwd(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["dout"], None, None, clamp=True)
+    for k, name in GRADS:
+        _close(name, g[k], r[name], torch.float16)
+
+
+def test_streaming_equals_full_pass(dev):
+    """Chunks carried through h_prev -> h_last reproduce one full pass (reference
+    tests/test_selective_scan.py:148-193), here in fp32 with config-2 distributions."""
+    x = workloads.ssm_inputs(2, 1024, 256, dtype=torch.float32, seed=7, dout=False)
+    xd = {k: v.to(dev) for k, v in x.items()}
+    m = SelectiveScanCuda()
+    with torch.no_grad():
+        full, h_full = m.forward_with_state(xd["u"], xd["delta"], xd["A"], xd["B"], xd["C"], xd["D"])
+        h = None
+        outs = []
+        for s in range(0, 1024, 256):
+            sl = slice(s, s + 256)
+            o, h = m.forward_with_state(xd["u"][:, sl], xd["delta"][:, sl], xd["A"], xd["B"][:, sl],
+                                        xd["C"][:, sl], xd["D"], h)
+            outs.append(o)
+    torch.testing.assert_close(torch.cat(outs, 1), full, rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(h, h_full, rtol=1e-5, atol=1e-6)
+
+
+def test_stateful_gradient_chain(dev):
+    """Gradients flow through h_last -> h_prev across two chunks exactly like one pass."""
+    x = workloads.ssm_inputs(1, 96, 40, dtype=torch.float32, seed=8)
+    xd = {k: v.to(dev).requires_grad_(k != "dout") for k, v in x.items()}
+    m = SelectiveScanCuda()
+    o1, h1 = m.forward_with_state(xd["u"][:, :50], xd["delta"][:, :50], xd["A"], xd["B"][:, :50],
+                                  xd["C"][:, :50], xd["D"])
+    o2, _ = m.forward_with_state(xd["u"][:, 50:], xd["delta"][:, 50:], xd["A"], xd["B"][:, 50:],
+                                 xd["C"][:, 50:], xd["D"], h1)
+    (torch.cat([o1, o2], 1) * xd["dout"]).sum().backward()
+    r = orc.ssm_bwd(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["dout"], None, None, clamp=True)
+    for k, name in GRADS:
+        _close(name, xd[k].grad, r[name], torch.float32)
+
+
+def test_extreme_delta_is_finite_and_matches(dev):
+    """delta = 10 with A = -U(0, 0.1), fp16 (reference test_numerical_stability_extreme_values,
+    tests/test_selective_scan.py:264-285)."""
+    x = workloads.ssm_inputs(1, 512, 64, dtype=torch.float16, a_lo=0.0, a_hi=0.1, seed=9, dout=False)
+    x["delta"] = torch.full_like(x["delta"], 10.0)
+    out, h_last, _ = _run(x, dev, with_h=False, grads=False)
+    assert torch.isfinite(out).all() and torch.isfinite(h_last).all()
+    ro, rh = orc.ssm_fwd(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], None, clamp=True)
+    _close("out", out, ro, torch.float16)
+
+
+def test_exp_argument_clamp(dev):
+    """delta*A = 120 is clamped to 88 before exp (mamba_cuda.py:65-70): with two steps the
+    state stays finite (e^88 * tiny), where an unclamped fp32 exp(120) would be inf."""
+    x = workloads.ssm_inputs(1, 2, 64, dtype=torch.float32, seed=9, dout=False)
+    x["delta"] = torch.full_like(x["delta"], 10.0)
+    x["A"][0, 0] = 12.0
+    x["u"] = x["u"] * 1e-30
+    out, h_last, _ = _run(x, dev, with_h=False, grads=False)
+    assert torch.isfinite(out).all() and torch.isfinite(h_last).all()
+    ro, rh = orc.ssm_fwd(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], None, clamp=True)
+    assert np.isfinite(rh).all() and abs(rh[0, 0, 0]) > 1.0  # the clamp is live
+    _close("out", out, ro, torch.float32)
+    _close("h_last", h_last, rh, torch.float32)
+
+
+def test_input_validation_on_device(dev):
+    """reference tests/test_selective_scan.py:239-262: wrong h_prev N or batch -> RuntimeError."""
+    x = {k: v.to(dev) for k, v in workloads.ssm_inputs(1, 64, 32, dtype=torch.float16, dout=False).items()}
+    m = SelectiveScanCuda()
+    with pytest.raises(RuntimeError):
+        m(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], torch.randn(1, 32, 17, device=dev).half())
+    with pytest.raises(RuntimeError):
+        m(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], torch.randn(2, 32, 16, device=dev).half())
+
+
+def test_no_grad_forward_keeps_nothing(dev):
+    x = {k: v.to(dev) for k, v in workloads.ssm_inputs(2, 512, 512, dtype=torch.float16, dout=False).items()}
+    m = SelectiveScanCuda()
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated()
+    with torch.no_grad():
+        out = m(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"])
+    torch.cuda.synchronize()
+    assert torch.cuda.memory_allocated() - base <= out.numel() * out.element_size() + 4096

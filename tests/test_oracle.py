@@ -13,18 +13,18 @@ import torch
 from oracle import oracle as orc
 from oracle import torch_ref
 
-torch.set_default_dtype(torch.float64)
+F64 = torch.float64
 
 
 def _inputs(bsz, L, dm, n=16, seed=0, a_lo=0.01, a_hi=1.0, h_prev=True):
     g = torch.Generator().manual_seed(seed)
-    u = torch.randn(bsz, L, dm, generator=g)
-    delta = 1e-3 + (1e-1 - 1e-3) * torch.rand(bsz, L, dm, generator=g)
-    A = -(a_lo + (a_hi - a_lo) * torch.rand(dm, n, generator=g))
-    B = torch.randn(bsz, L, n, generator=g)
-    C = torch.randn(bsz, L, n, generator=g)
-    D = 1.0 + 0.1 * torch.randn(dm, generator=g)
-    hp = 0.1 * torch.randn(bsz, dm, n, generator=g) if h_prev else None
+    u = torch.randn(bsz, L, dm, generator=g, dtype=F64)
+    delta = 1e-3 + (1e-1 - 1e-3) * torch.rand(bsz, L, dm, generator=g, dtype=F64)
+    A = -(a_lo + (a_hi - a_lo) * torch.rand(dm, n, generator=g, dtype=F64))
+    B = torch.randn(bsz, L, n, generator=g, dtype=F64)
+    C = torch.randn(bsz, L, n, generator=g, dtype=F64)
+    D = 1.0 + 0.1 * torch.randn(dm, generator=g, dtype=F64)
+    hp = 0.1 * torch.randn(bsz, dm, n, generator=g, dtype=F64) if h_prev else None
     return u, delta, A, B, C, D, hp
 
 
@@ -44,13 +44,13 @@ def test_fwd_matches_closed_form():
     # the reference tests' own oracle: benign |A*cumsum(delta)|
     g = torch.Generator().manual_seed(3)
     bsz, L, dm, n = 2, 256, 24, 16
-    u = 0.1 * torch.randn(bsz, L, dm, generator=g)
-    delta = torch.full((bsz, L, dm), 0.01)
-    A = -0.1 * torch.rand(dm, n, generator=g)
-    B = 0.1 * torch.randn(bsz, L, n, generator=g)
-    C = 0.1 * torch.randn(bsz, L, n, generator=g)
-    D = torch.full((dm,), 0.1)
-    hp = torch.randn(bsz, dm, n, generator=g)
+    u = 0.1 * torch.randn(bsz, L, dm, generator=g, dtype=F64)
+    delta = torch.full((bsz, L, dm), 0.01, dtype=F64)
+    A = -0.1 * torch.rand(dm, n, generator=g, dtype=F64)
+    B = 0.1 * torch.randn(bsz, L, n, generator=g, dtype=F64)
+    C = 0.1 * torch.randn(bsz, L, n, generator=g, dtype=F64)
+    D = torch.full((dm,), 0.1, dtype=F64)
+    hp = torch.randn(bsz, dm, n, generator=g, dtype=F64)
     out, hl = orc.ssm_fwd(u, delta, A, B, C, D, hp)
     co, ch = torch_ref.selective_scan_closed(u, delta, A, B, C, D, hp)
     np.testing.assert_allclose(out, co.numpy(), rtol=1e-9, atol=1e-11)
@@ -106,8 +106,8 @@ def test_fwd_clamp_semantics():
 def test_bwd_matches_autograd(shape, with_h):
     u, delta, A, B, C, D, hp = _inputs(*shape, seed=11 + sum(shape), h_prev=with_h)
     g = torch.Generator().manual_seed(99)
-    dout = torch.randn(u.shape, generator=g)
-    dhl = torch.randn(shape[0], shape[2], shape[3], generator=g) if with_h else None
+    dout = torch.randn(u.shape, generator=g, dtype=F64)
+    dhl = torch.randn(shape[0], shape[2], shape[3], generator=g, dtype=F64) if with_h else None
     leaves = [x.clone().requires_grad_(True) for x in (u, delta, A, B, C, D)]
     hpl = hp.clone().requires_grad_(True) if with_h else None
     out, hl = torch_ref.selective_scan_seq(*leaves, hpl)
@@ -125,8 +125,8 @@ def test_bwd_finite_differences():
     bsz, L, dm, n = 2, 6, 3, 4
     u, delta, A, B, C, D, hp = _inputs(bsz, L, dm, n, seed=21)
     g = torch.Generator().manual_seed(5)
-    dout = torch.randn(bsz, L, dm, generator=g)
-    dhl = torch.randn(bsz, dm, n, generator=g)
+    dout = torch.randn(bsz, L, dm, generator=g, dtype=F64)
+    dhl = torch.randn(bsz, dm, n, generator=g, dtype=F64)
     args = [x.numpy().copy() for x in (u, delta, A, B, C, D, hp)]
     names = ["du", "ddelta", "dA", "dB", "dC", "dD", "dh_prev"]
     r = orc.ssm_bwd(*args[:6], dout, args[6], dhl)
@@ -149,7 +149,7 @@ def test_bwd_finite_differences():
 
 def test_bwd_closed_form_identities():
     u, delta, A, B, C, D, hp = _inputs(2, 50, 11, seed=8)
-    dout = torch.randn(u.shape, generator=torch.Generator().manual_seed(1))
+    dout = torch.randn(u.shape, generator=torch.Generator().manual_seed(1), dtype=F64)
     r = orc.ssm_bwd(u, delta, A, B, C, D, dout, hp, None)
     # dD = sum_{b,t} dout*u
     np.testing.assert_allclose(r["dD"], (dout * u).sum((0, 1)).numpy(), rtol=1e-12)
@@ -164,7 +164,7 @@ def test_bwd_closed_form_identities():
 
 def test_bwd_deterministic():
     u, delta, A, B, C, D, hp = _inputs(2, 40, 150, seed=4)
-    dout = torch.randn(u.shape, generator=torch.Generator().manual_seed(2))
+    dout = torch.randn(u.shape, generator=torch.Generator().manual_seed(2), dtype=F64)
     r1 = orc.ssm_bwd(u, delta, A, B, C, D, dout, hp, None)
     r2 = orc.ssm_bwd(u, delta, A, B, C, D, dout, hp, None)
     for k in r1:
@@ -174,15 +174,15 @@ def test_bwd_deterministic():
 @pytest.mark.parametrize("shape", [(2, 3, 50, 4), (1, 1, 1, 7), (4, 1000, 8)])
 def test_pscan_matches_sequential(shape):
     g = torch.Generator().manual_seed(7)
-    A = 0.9 + 0.1 * torch.rand(shape, generator=g)
-    X = torch.randn(shape, generator=g)
+    A = 0.9 + 0.1 * torch.rand(shape, generator=g, dtype=F64)
+    X = torch.randn(shape, generator=g, dtype=F64)
     H = orc.pscan_fwd(A, X)
     np.testing.assert_allclose(H, torch_ref.pscan_seq(A, X).numpy(), rtol=1e-12, atol=1e-12)
 
 
 def test_pscan_special_cases():
     g = torch.Generator().manual_seed(8)
-    X = torch.randn(3, 2, 64, 5, generator=g)
+    X = torch.randn(3, 2, 64, 5, generator=g, dtype=F64)
     # A = 1 -> cumsum
     np.testing.assert_allclose(orc.pscan_fwd(torch.ones_like(X), X), torch.cumsum(X, 2).numpy(), rtol=1e-12, atol=1e-12)
     # A = 0 -> X
@@ -194,7 +194,7 @@ def test_pscan_special_cases():
     W = torch.tril(a ** (t.view(-1, 1) - t.view(1, -1)))
     np.testing.assert_allclose(H, torch.einsum("ts,bdsn->bdtn", W, X).numpy(), rtol=1e-10, atol=1e-12)
     # A_0 has no effect
-    A = torch.rand(X.shape, generator=g)
+    A = torch.rand(X.shape, generator=g, dtype=F64)
     A2 = A.clone()
     A2[:, :, 0] = 123.0
     np.testing.assert_array_equal(orc.pscan_fwd(A, X), orc.pscan_fwd(A2, X))
@@ -202,9 +202,9 @@ def test_pscan_special_cases():
 
 def test_pscan_bwd_matches_autograd():
     g = torch.Generator().manual_seed(10)
-    A = (0.5 + 0.5 * torch.rand(2, 3, 37, 4, generator=g)).requires_grad_(True)
-    X = torch.randn(2, 3, 37, 4, generator=g).requires_grad_(True)
-    dH = torch.randn(2, 3, 37, 4, generator=g)
+    A = (0.5 + 0.5 * torch.rand(2, 3, 37, 4, generator=g, dtype=F64)).requires_grad_(True)
+    X = torch.randn(2, 3, 37, 4, generator=g, dtype=F64).requires_grad_(True)
+    dH = torch.randn(2, 3, 37, 4, generator=g, dtype=F64)
     H = torch_ref.pscan_seq(A, X)
     (H * dH).sum().backward()
     dA, dX = orc.pscan_bwd(A.detach(), H.detach(), dH)
