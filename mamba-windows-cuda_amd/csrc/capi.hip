@@ -65,13 +65,15 @@ int choose_spl(int64_t channels) {
     return 1;
 }
 
-size_t fwd_workspace_bytes(const SsmShape& s) { return align256((size_t)s.batch * s.seqlen * 32 * sizeof(float)); }
+size_t fwd_workspace_bytes(const SsmShape& s) {
+    (void)s;
+    return 0;  // the forward stages its inputs through LDS and needs no scratch
+}
 
 size_t bwd_workspace_bytes(const SsmShape& s) {
     const int spl = choose_spl(s.batch * s.dim);
     const int ngrp = bwd_groups(s, spl);
-    size_t n = fwd_workspace_bytes(s);
-    n += align256((size_t)ngrp * s.batch * s.seqlen * 32 * sizeof(float));  // dB/dC partials
+    size_t n = align256((size_t)ngrp * s.batch * s.seqlen * 32 * sizeof(float));  // dB/dC partials
     n += align256((size_t)s.batch * s.dim * kNState * sizeof(float));         // dA partials
     n += align256((size_t)s.batch * s.dim * sizeof(float));                   // dD partials
     return n;
@@ -121,15 +123,12 @@ int mwc_ssm_fwd(int dtype, const void* u, const void* delta, const void* A, cons
     if (seqlen > 0 && (!u || !delta || !B_ssm || !C_ssm))
         return fail(MWC_ERR_INVALID_ARGUMENT, "u, delta, B_ssm and C_ssm must not be NULL");
     const mwc::SsmShape s{batch, seqlen, dim};
-    const size_t need = mwc::fwd_workspace_bytes(s);
-    if (seqlen > 0 && (workspace == nullptr || workspace_bytes < need))
-        return fail(MWC_ERR_WORKSPACE, "forward workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+    (void)workspace;
+    (void)workspace_bytes;
     const bool half = dtype == MWC_DTYPE_F16;
     hipStream_t st = (hipStream_t)stream;
-    float* bc = (float*)workspace;
-    if (seqlen > 0) MWC_HIP_TRY(mwc::launch_pack_bc(half, B_ssm, C_ssm, bc, batch * seqlen, st));
     const int spl = mwc::choose_spl(batch * dim);
-    MWC_HIP_TRY(mwc::launch_ssm_fwd(half, spl, u, delta, A, bc, D_ssm, h_prev, out, h_last, ckpt, s, st));
+    MWC_HIP_TRY(mwc::launch_ssm_fwd(half, spl, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, out, h_last, ckpt, s, st));
     return MWC_OK;
 }
 
@@ -155,15 +154,12 @@ int mwc_ssm_bwd(int dtype, const void* u, const void* delta, const void* A, cons
     const int spl = mwc::choose_spl(batch * dim);
     const int ngrp = mwc::bwd_groups(s, spl);
     char* w = (char*)workspace;
-    float* bc = (float*)w;
-    w += mwc::fwd_workspace_bytes(s);
     float* dbc_part = (float*)w;
     w += align256((size_t)ngrp * batch * seqlen * 32 * sizeof(float));
     float* dA_part = (float*)w;
     w += align256((size_t)batch * dim * mwc::kNState * sizeof(float));
     float* dD_part = (float*)w;
-    if (seqlen > 0) MWC_HIP_TRY(mwc::launch_pack_bc(half, B_ssm, C_ssm, bc, batch * seqlen, st));
-    MWC_HIP_TRY(mwc::launch_ssm_bwd(half, spl, u, delta, A, bc, D_ssm, dout, dh_last, ckpt, du, ddelta, dh_prev,
+    MWC_HIP_TRY(mwc::launch_ssm_bwd(half, spl, u, delta, A, B_ssm, C_ssm, D_ssm, dout, dh_last, ckpt, du, ddelta, dh_prev,
                                     dA_part, dD_part, dbc_part, s, st));
     MWC_HIP_TRY(mwc::launch_bwd_finish(half, dbc_part, dA_part, dD_part, dB, dC, dA, dD, ngrp, s, st));
     return MWC_OK;

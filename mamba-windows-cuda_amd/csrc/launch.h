@@ -19,13 +19,11 @@ size_t bwd_workspace_bytes(const SsmShape& s);
 int bwd_groups(const SsmShape& s, int spl);  // channel groups that write dB/dC partials
 
 // Kernel launchers; `is_half` selects fp16 storage. They only enqueue work.
-hipError_t launch_pack_bc(bool is_half, const void* B, const void* C, float* bc, int64_t rows,
-                          hipStream_t st);
 hipError_t launch_ssm_fwd(bool is_half, int spl, const void* u, const void* delta, const void* A,
-                          const float* bc, const void* Dv, const void* h_prev, void* out,
+                          const void* B, const void* C, const void* Dv, const void* h_prev, void* out,
                           void* h_last, float* ckpt, const SsmShape& s, hipStream_t st);
 hipError_t launch_ssm_bwd(bool is_half, int spl, const void* u, const void* delta, const void* A,
-                          const float* bc, const void* Dv, const void* dout, const void* dh_last,
+                          const void* B, const void* C, const void* Dv, const void* dout, const void* dh_last,
                           const float* ckpt, void* du, void* ddelta, void* dh_prev, float* dA_part,
                           float* dD_part, float* dbc_part, const SsmShape& s, hipStream_t st);
 hipError_t launch_bwd_finish(bool is_half, const float* dbc_part, const float* dA_part,

@@ -11,18 +11,22 @@
 //   dB     = sum_d g*delta*u                      dC = sum_d dout*h_t
 //   dh_prev = dA_0*g_0
 //
-// Mapping: the forward's lane groups (LPC lanes x SPL states per channel).
-// The sequence is walked in reverse in chunks of kCkptSteps steps; each chunk
-// restarts from the fp32 checkpoint the forward stored, recomputes the chunk's
-// states and decay factors into VGPRs (one exp per state), then runs the
-// reverse sweep. Sums over n (du, ddelta) are DPP reductions inside the lane
-// group. Sums over channels (dB, dC) go through LDS: every 4 steps each wave
-// folds its channels in its own LDS slab (no barrier -- LDS operations of one
-// wave complete in order), and once per chunk the workgroup's waves are
-// summed and written as a per-group fp32 partial; a second small kernel adds
-// the groups in fixed order, so the result is deterministic (no atomics).
-// dA and dD accumulate in registers over (t) and are summed over b by the
-// finishing kernel.
+// Mapping: the forward's lane groups (LPC lanes x SPL states per channel, 4
+// waves = CPB channels of one batch row per workgroup). The sequence is walked
+// in reverse in chunks of 16 steps; each chunk restarts from the fp32
+// checkpoint the forward stored, recomputes the chunk's states and decay
+// factors into VGPRs (one exp per state) and runs the reverse sweep. Inputs
+// are staged through LDS exactly as in the forward (fp32 delta, delta*u, u,
+// dout rows per channel; B/C rows per step), double-buffered with the previous
+// chunk's global loads in flight. Sums over n (du, ddelta) are DPP reductions
+// inside the lane group. Sums over channels (dB, dC) go through a wave-private
+// LDS slab: each step the lanes deposit g_t and h_t, and every 4 steps the
+// wave folds its channels with one FMA per state against the per-channel
+// weights (delta*u for dB, dout for dC) read from the staged tile; once per
+// chunk the workgroup's waves are added and written as a per-group fp32
+// partial, which a second small kernel sums in fixed order (deterministic, no
+// atomics). dA and dD accumulate in registers over t and are summed over b by
+// the finishing kernel.
 #include "common.h"
 #include "launch.h"
 
@@ -30,12 +34,11 @@ namespace mwc {
 
 namespace {
 
-constexpr int kWpb = 4;       // waves per workgroup in the backward
 constexpr int kRedSlots = 4;  // steps folded per in-wave LDS reduction
-constexpr int kRowPad = 36;   // floats per channel row in the LDS slab (32 values + pad)
+constexpr int kRowPad = 36;   // floats per channel row of the slab (16 g + 16 h + pad)
 
 template <int K>
-__device__ __forceinline__ void ldv(const float* __restrict__ p, float (&v)[K]) {
+__device__ __forceinline__ void ldv(const float* p, float (&v)[K]) {
     if constexpr (K % 4 == 0) {
 #pragma unroll
         for (int k = 0; k < K; k += 4) {
@@ -66,35 +69,62 @@ __device__ __forceinline__ void stv(float* p, const float (&v)[K]) {
     }
 }
 
+// Orders this wave's LDS traffic for the compiler; one wave's LDS operations
+// are executed in issue order by the hardware.
+__device__ __forceinline__ void wave_lds_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 }  // namespace
 
 template <typename T, int SPL>
-__global__ void __launch_bounds__(64 * kWpb) ssm_bwd_kernel(
-    const T* __restrict__ u, const T* __restrict__ delta, const T* __restrict__ A, const float* __restrict__ bc,
-    const T* __restrict__ Dv, const T* __restrict__ dout, const T* __restrict__ dh_last,
+__global__ void __launch_bounds__(256) ssm_bwd_kernel(
+    const T* __restrict__ u, const T* __restrict__ delta, const T* __restrict__ A, const T* __restrict__ Bm,
+    const T* __restrict__ Cm, const T* __restrict__ Dv, const T* __restrict__ dout, const T* __restrict__ dh_last,
     const float* __restrict__ ckpt, T* __restrict__ du, T* __restrict__ ddelta, T* __restrict__ dh_prev,
     float* __restrict__ dA_part, float* __restrict__ dD_part, float* __restrict__ dbc_part, int Bsz, int L, int D,
-    int nck, int ngrp) {
+    int nck, int nblk_d) {
     constexpr int LPC = kNState / SPL;
     constexpr int CPW = 64 / LPC;
+    constexpr int CPB = CPW * 4;
     constexpr int TC = kCkptSteps;
-    constexpr int HALF = CPW / 2;  // channels each reducing lane folds
-    static_assert(CPW >= 2, "reduction needs two channel halves");
+    constexpr int RS = TC + 4;
+    constexpr int NSG = 256 / CPB;
+    constexpr int SPG = TC / NSG;
+    constexpr int OS = CPB + 4;
+    constexpr int HALF = CPW / 2;  // channels each folding lane sums
+    static_assert(NSG * SPG == TC && CPW >= 2, "tiling");
 
-    __shared__ float red[kWpb][kRedSlots][CPW][kRowPad];
-    __shared__ float wsum[2][kWpb][TC][32];
+    __shared__ float s_in[2][4][CPB][RS];  // [buf][delta, delta*u, u, dout][channel][step]
+    __shared__ float s_bc[2][TC][2 * kNState];
+    __shared__ float s_red[4][kRedSlots][CPW][kRowPad];
+    __shared__ float s_part[2][4][TC][2 * kNState];
+    __shared__ float s_out[2][2][TC][OS];  // [buf][du, ddelta][step][channel]
 
+    const int tid = threadIdx.x;
     const int lid = xcd_remap(blockIdx.x, gridDim.x);
-    const int b = lid / ngrp;
-    const int grp = lid % ngrp;
-    const int wave = threadIdx.x / 64;
-    const int lane = threadIdx.x % 64;
-    const int c = lane / LPC, g = lane % LPC;
-    const int d_raw = (grp * kWpb + wave) * CPW + c;
-    const bool valid = d_raw < D;
-    const int d = valid ? d_raw : D - 1;
+    const int b = lid / nblk_d;
+    const int blk = lid % nblk_d;
+    const int d0 = blk * CPB;
+
+    const int wave = tid >> 6, lane = tid & 63;
+    const int cw = lane / LPC;  // channel within the wave
+    const int c = wave * CPW + cw;
+    const int g = lane % LPC;
     const int n0 = g * SPL;
-    const float vmask = valid ? 1.f : 0.f;  // padded lanes contribute nothing to dB/dC
+    const bool valid = d0 + c < D;
+    const int d = valid ? d0 + c : D - 1;
+
+    const int lc = tid % CPB, sg = tid / CPB;
+    const bool lvalid = d0 + lc < D;
+    const int ld_d = lvalid ? d0 + lc : D - 1;
+    const int bc_t = tid >> 4, bc_n = tid & 15;
+    const int64_t row0 = (int64_t)b * L;
+
+    // folding roles: slot rs (step i+rs), value quad q (dB n=4q.. for q<4, dC for q>=4), channel half
+    const int rs = lane >> 4, rq = (lane >> 1) & 7, rhalf = lane & 1;
 
     float A2[SPL], An[SPL], gc[SPL], dAacc[SPL];
 #pragma unroll
@@ -106,107 +136,164 @@ __global__ void __launch_bounds__(64 * kWpb) ssm_bwd_kernel(
     }
     float dDacc = 0.f;
     const float Dd = ld(Dv + d);
-    const int64_t base = (int64_t)b * L * D + d;
-    const float* __restrict__ bcb = bc + (int64_t)b * L * 32 + n0;
-    const float* __restrict__ ckb = ckpt + ((int64_t)b * nck * D + d) * kNState + n0;
+    const float* ckb = ckpt + ((int64_t)b * nck * D + d) * kNState + n0;
 
-    // reduction lane roles: pair p = lane/2 -> (slot, value quad), half = lane&1
-    const int rp = lane >> 1, rhalf = lane & 1;
-    const int rslot = rp >> 3, rq = rp & 7;
-    float(*myred)[CPW][kRowPad] = red[wave];
+    T pu[SPG], pd[SPG], py[SPG], pb, pc;
+    float hnext[SPL];
+    auto issue = [&](int k) {
+#pragma unroll
+        for (int s = 0; s < SPG; ++s) {
+            const int t = min(k * TC + sg * SPG + s, L - 1);
+            const int64_t off = (row0 + t) * D + ld_d;
+            pu[s] = u[off];
+            pd[s] = delta[off];
+            py[s] = dout[off];
+        }
+        const int t = min(k * TC + bc_t, L - 1);
+        pb = Bm[(row0 + t) * kNState + bc_n];
+        pc = Cm[(row0 + t) * kNState + bc_n];
+        ldv<SPL>(ckb + (int64_t)k * D * kNState, hnext);
+    };
+    auto commit = [&](int k, int buf) {
+        float vd[SPG], vdu[SPG], vu[SPG], vy[SPG];
+#pragma unroll
+        for (int s = 0; s < SPG; ++s) {
+            const bool ok = lvalid && (k * TC + sg * SPG + s < L);
+            vd[s] = ok ? static_cast<float>(pd[s]) : 0.f;
+            vu[s] = ok ? static_cast<float>(pu[s]) : 0.f;
+            vy[s] = ok ? static_cast<float>(py[s]) : 0.f;
+            vdu[s] = vd[s] * vu[s];
+        }
+        stv<SPG>(&s_in[buf][0][lc][sg * SPG], vd);
+        stv<SPG>(&s_in[buf][1][lc][sg * SPG], vdu);
+        stv<SPG>(&s_in[buf][2][lc][sg * SPG], vu);
+        stv<SPG>(&s_in[buf][3][lc][sg * SPG], vy);
+        s_bc[buf][bc_t][bc_n] = static_cast<float>(pb);
+        s_bc[buf][bc_t][kNState + bc_n] = static_cast<float>(pc);
+    };
+
+    float hin[SPL];
+    if (nck > 0) {  // L == 0 has no chunk; the outputs below are then dh_prev = dh_last and zero partials
+        issue(nck - 1);
+        commit(nck - 1, (nck - 1) & 1);
+#pragma unroll
+        for (int j = 0; j < SPL; ++j) hin[j] = hnext[j];
+    }
+    __syncthreads();
+
+    float(*red)[CPW][kRowPad] = s_red[wave];
 
     for (int k = nck - 1; k >= 0; --k) {
+        const int buf = k & 1;
         const int t0 = k * TC;
-        const int tn = min(TC, L - t0);
-        float hin[SPL];
-        ldv<SPL>(ckb + (int64_t)k * D * kNState, hin);
+        if (k > 0) issue(k - 1);
 
-        float H[TC][SPL], E[TC][SPL], DT[TC], UT[TC], YO[TC];
         // ---- recompute the chunk's states (one exp per state) ----
+        float H[TC][SPL], E[TC][SPL], dt[TC];
         {
+            float dtu[TC];
+            ldv<TC>(&s_in[buf][0][c][0], dt);
+            ldv<TC>(&s_in[buf][1][c][0], dtu);
             float hh[SPL];
 #pragma unroll
             for (int j = 0; j < SPL; ++j) hh[j] = hin[j];
 #pragma unroll
             for (int i = 0; i < TC; ++i) {
-                if (i < tn) {
-                    const int64_t t = t0 + i;
-                    DT[i] = ld(delta + base + t * D);
-                    UT[i] = ld(u + base + t * D);
-                    YO[i] = ld(dout + base + t * D) * vmask;
-                    float Bv[SPL];
-                    ldv<SPL>(bcb + t * 32, Bv);
-                    const float dtu = DT[i] * UT[i];
+                float Bv[SPL];
+                ldv<SPL>(&s_bc[buf][i][n0], Bv);
 #pragma unroll
-                    for (int j = 0; j < SPL; ++j) {
-                        E[i][j] = exp2_clamped(DT[i] * A2[j]);
-                        hh[j] = __builtin_fmaf(E[i][j], hh[j], dtu * Bv[j]);
-                        H[i][j] = hh[j];
-                    }
+                for (int j = 0; j < SPL; ++j) {
+                    E[i][j] = exp2_clamped(dt[i] * A2[j]);
+                    hh[j] = __builtin_fmaf(E[i][j], hh[j], dtu[i] * Bv[j]);
+                    H[i][j] = hh[j];
                 }
             }
         }
         // ---- reverse sweep ----
+        float uq[4], yq[4];
 #pragma unroll
         for (int i = TC - 1; i >= 0; --i) {
-            const int slot = i % kRedSlots;
-            float dBv[SPL], dCv[SPL];
-            if (i < tn) {
-                const int64_t t = t0 + i;
-                float Bv[SPL], Cv[SPL];
-                ldv<SPL>(bcb + t * 32, Bv);
-                ldv<SPL>(bcb + t * 32 + kNState, Cv);
-                const float yo = YO[i];
-                const float dtu = DT[i] * UT[i] * vmask;
-                float r1 = 0.f, r2 = 0.f;
-#pragma unroll
-                for (int j = 0; j < SPL; ++j) {
-                    const float prev = (i > 0) ? H[i > 0 ? i - 1 : 0][j] : hin[j];
-                    const float gt = __builtin_fmaf(yo, Cv[j], gc[j]);
-                    dCv[j] = yo * H[i][j];
-                    dBv[j] = gt * dtu;
-                    r1 = __builtin_fmaf(gt, Bv[j], r1);
-                    const float s = gt * E[i][j] * prev;
-                    r2 = __builtin_fmaf(An[j], s, r2);
-                    dAacc[j] = __builtin_fmaf(DT[i], s, dAacc[j]);
-                    gc[j] = E[i][j] * gt;
-                }
-                r1 = group_sum<LPC>(r1);
-                r2 = group_sum<LPC>(r2);
-                if (g == 0 && valid) {
-                    st(du + base + t * D, __builtin_fmaf(Dd, yo, DT[i] * r1));
-                    st(ddelta + base + t * D, __builtin_fmaf(UT[i], r1, r2));
-                }
-                dDacc = __builtin_fmaf(yo, UT[i], dDacc);
-            } else {
-#pragma unroll
-                for (int j = 0; j < SPL; ++j) dBv[j] = dCv[j] = 0.f;
+            if (i % 4 == 3) {
+                ldv<4>(&s_in[buf][2][c][i - 3], uq);
+                ldv<4>(&s_in[buf][3][c][i - 3], yq);
             }
-            stv<SPL>(&myred[slot][c][n0], dBv);
-            stv<SPL>(&myred[slot][c][kNState + n0], dCv);
+            const float ui = uq[i % 4], yo = yq[i % 4];
+            float Bv[SPL], Cv[SPL];
+            ldv<SPL>(&s_bc[buf][i][n0], Bv);
+            ldv<SPL>(&s_bc[buf][i][kNState + n0], Cv);
+            float gt[SPL];
+            float r1 = 0.f, r2 = 0.f;
+#pragma unroll
+            for (int j = 0; j < SPL; ++j) {
+                const float prev = (i > 0) ? H[i > 0 ? i - 1 : 0][j] : hin[j];
+                gt[j] = __builtin_fmaf(yo, Cv[j], gc[j]);
+                r1 = __builtin_fmaf(gt[j], Bv[j], r1);
+                const float s = gt[j] * E[i][j] * prev;
+                r2 = __builtin_fmaf(An[j], s, r2);
+                dAacc[j] = __builtin_fmaf(dt[i], s, dAacc[j]);
+                gc[j] = E[i][j] * gt[j];
+            }
+            r1 = group_sum<LPC>(r1);
+            r2 = group_sum<LPC>(r2);
+            // every lane of the group holds the sums; duplicate LDS writes are identical
+            s_out[buf][0][i][c] = __builtin_fmaf(Dd, yo, dt[i] * r1);
+            s_out[buf][1][i][c] = __builtin_fmaf(ui, r1, r2);
+            dDacc = __builtin_fmaf(yo, ui, dDacc);
+            const int slot = i % kRedSlots;
+            stv<SPL>(&red[slot][cw][n0], gt);
+            stv<SPL>(&red[slot][cw][kNState + n0], H[i]);
             if (slot == 0) {
-                // fold this wave's channels for steps i..i+3 (values 4*rq..4*rq+3 of slot rslot)
+                wave_lds_fence();
+                // fold this wave's channels for steps i..i+3: weight delta*u (dB) or dout (dC)
+                const int wsel = rq < 4 ? 1 : 3;
+                const float* wrow = &s_in[buf][wsel][wave * CPW][i + rs];
                 float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int m = 0; m < HALF; ++m) {
+                    const int ch = rhalf * HALF + m;
                     float v4[4];
-                    ldv<4>(&myred[rslot][rhalf * HALF + m][rq * 4], v4);
+                    ldv<4>(&red[rs][ch][rq * 4], v4);
+                    const float wgt = wrow[ch * RS];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) acc[q] += v4[q];
+                    for (int q = 0; q < 4; ++q) acc[q] = __builtin_fmaf(v4[q], wgt, acc[q]);
                 }
 #pragma unroll
                 for (int q = 0; q < 4; ++q) acc[q] += dpp<kDppXor1>(acc[q]);
-                if (rhalf == 0) stv<4>(&wsum[k & 1][wave][i + rslot][rq * 4], acc);
+                if (rhalf == 0) stv<4>(&s_part[buf][wave][i + rs][rq * 4], acc);
+                wave_lds_fence();
             }
         }
-        __syncthreads();
-        // sum the workgroup's waves and emit this group's partial for the chunk
-        for (int o = threadIdx.x; o < TC * 32; o += 64 * kWpb) {
-            const int tt = o / 32;
-            float s = 0.f;
+        if (k > 0) {
+            commit(k - 1, buf ^ 1);
 #pragma unroll
-            for (int w = 0; w < kWpb; ++w) s += wsum[k & 1][w][tt][o % 32];
-            if (tt < tn) dbc_part[(((int64_t)grp * Bsz + b) * L + t0 + tt) * 32 + (o % 32)] = s;
+            for (int j = 0; j < SPL; ++j) hin[j] = hnext[j];
+        }
+        __syncthreads();
+        // coalesced du / ddelta tile stores: thread -> (step, VPT channels)
+        {
+            constexpr int VPT = CPB / 16;
+            const int st_ = tid >> 4, cq = (tid & 15) * VPT;
+            const int t = t0 + st_;
+            if (t < L) {
+                float a[VPT], bb[VPT];
+                ldv<VPT>(&s_out[buf][0][st_][cq], a);
+                ldv<VPT>(&s_out[buf][1][st_][cq], bb);
+                T* pdu = du + (row0 + t) * D + d0 + cq;
+                T* pdd = ddelta + (row0 + t) * D + d0 + cq;
+#pragma unroll
+                for (int q = 0; q < VPT; ++q)
+                    if (d0 + cq + q < D) {
+                        pdu[q] = static_cast<T>(a[q]);
+                        pdd[q] = static_cast<T>(bb[q]);
+                    }
+            }
+        }
+        // this workgroup's dB/dC partial for the chunk (sum of its 4 waves)
+        for (int o = tid; o < TC * 2 * kNState; o += 256) {
+            const int tt = o >> 5, v = o & 31;
+            const float s = s_part[buf][0][tt][v] + s_part[buf][1][tt][v] + s_part[buf][2][tt][v] +
+                            s_part[buf][3][tt][v];
+            if (t0 + tt < L) dbc_part[(((int64_t)blk * Bsz + b) * L + t0 + tt) * 32 + v] = s;
         }
     }
 
@@ -256,34 +343,34 @@ __global__ void __launch_bounds__(256) bwd_finish_ad_kernel(const float* __restr
 }
 
 int bwd_groups(const SsmShape& s, int spl) {
-    const int cpw = 64 / (kNState / spl);
-    const int per_wg = cpw * kWpb;
-    return (int)((s.dim + per_wg - 1) / per_wg);
+    const int cpb = 4 * 64 / (kNState / spl);
+    return (int)((s.dim + cpb - 1) / cpb);
 }
 
 template <typename T, int SPL>
-static hipError_t bwd_inst(const void* u, const void* delta, const void* A, const float* bc, const void* Dv,
-                           const void* dout, const void* dh_last, const float* ckpt, void* du, void* ddelta,
-                           void* dh_prev, float* dA_part, float* dD_part, float* dbc_part, const SsmShape& s,
-                           hipStream_t st) {
-    const int ngrp = bwd_groups(s, SPL);
+static hipError_t bwd_inst(const void* u, const void* delta, const void* A, const void* B, const void* C,
+                           const void* Dv, const void* dout, const void* dh_last, const float* ckpt, void* du,
+                           void* ddelta, void* dh_prev, float* dA_part, float* dD_part, float* dbc_part,
+                           const SsmShape& s, hipStream_t st) {
+    const int nblk_d = bwd_groups(s, SPL);
     const int nck = (int)((s.seqlen + kCkptSteps - 1) / kCkptSteps);
-    const int grid = ngrp * (int)s.batch;
-    hipLaunchKernelGGL((ssm_bwd_kernel<T, SPL>), dim3(grid), dim3(64 * kWpb), 0, st, (const T*)u, (const T*)delta,
-                       (const T*)A, bc, (const T*)Dv, (const T*)dout, (const T*)dh_last, ckpt, (T*)du, (T*)ddelta,
-                       (T*)dh_prev, dA_part, dD_part, dbc_part, (int)s.batch, (int)s.seqlen, (int)s.dim, nck, ngrp);
+    const int grid = nblk_d * (int)s.batch;
+    hipLaunchKernelGGL((ssm_bwd_kernel<T, SPL>), dim3(grid), dim3(256), 0, st, (const T*)u, (const T*)delta,
+                       (const T*)A, (const T*)B, (const T*)C, (const T*)Dv, (const T*)dout, (const T*)dh_last, ckpt,
+                       (T*)du, (T*)ddelta, (T*)dh_prev, dA_part, dD_part, dbc_part, (int)s.batch, (int)s.seqlen,
+                       (int)s.dim, nck, nblk_d);
     return hipGetLastError();
 }
 
-hipError_t launch_ssm_bwd(bool is_half, int spl, const void* u, const void* delta, const void* A, const float* bc,
-                          const void* Dv, const void* dout, const void* dh_last, const float* ckpt, void* du,
-                          void* ddelta, void* dh_prev, float* dA_part, float* dD_part, float* dbc_part,
+hipError_t launch_ssm_bwd(bool is_half, int spl, const void* u, const void* delta, const void* A, const void* B,
+                          const void* C, const void* Dv, const void* dout, const void* dh_last, const float* ckpt,
+                          void* du, void* ddelta, void* dh_prev, float* dA_part, float* dD_part, float* dbc_part,
                           const SsmShape& s, hipStream_t st) {
-#define MWC_BWD_SPL(S)                                                                                        \
-    if (spl == S)                                                                                             \
-        return is_half ? bwd_inst<half_t, S>(u, delta, A, bc, Dv, dout, dh_last, ckpt, du, ddelta, dh_prev,  \
-                                             dA_part, dD_part, dbc_part, s, st)                               \
-                       : bwd_inst<float, S>(u, delta, A, bc, Dv, dout, dh_last, ckpt, du, ddelta, dh_prev,   \
+#define MWC_BWD_SPL(S)                                                                                           \
+    if (spl == S)                                                                                                \
+        return is_half ? bwd_inst<half_t, S>(u, delta, A, B, C, Dv, dout, dh_last, ckpt, du, ddelta, dh_prev,   \
+                                             dA_part, dD_part, dbc_part, s, st)                                  \
+                       : bwd_inst<float, S>(u, delta, A, B, C, Dv, dout, dh_last, ckpt, du, ddelta, dh_prev,    \
                                             dA_part, dD_part, dbc_part, s, st);
     MWC_BWD_SPL(1)
     MWC_BWD_SPL(2)

@@ -52,8 +52,9 @@ def test_argument_errors_before_any_launch():
     # bad dtype
     st = L.mwc_ssm_fwd(7, fake, fake, fake, fake, fake, fake, None, fake, None, None, 1, 8, 8, 16, fake, 1 << 20, None)
     assert st == 1
-    # workspace too small
-    st = L.mwc_ssm_fwd(0, fake, fake, fake, fake, fake, fake, None, fake, None, None, 1, 8, 8, 16, fake, 4, None)
+    # backward workspace too small
+    st = L.mwc_ssm_bwd(0, fake, fake, fake, fake, fake, fake, None, fake, None, fake, fake, fake, fake, fake, fake,
+                       fake, None, 1, 8, 8, 16, fake, 4, None)
     assert st == 3 and b"workspace" in L.mwc_last_error()
     # backward without checkpoints
     st = L.mwc_ssm_bwd(0, fake, fake, fake, fake, fake, fake, None, fake, None, None, fake, fake, fake, fake, fake,
@@ -74,7 +75,7 @@ def test_workspace_sizes_monotone():
     a = L.mwc_ssm_bwd_workspace_size(8, 2048, 1536, 16)
     b = L.mwc_ssm_bwd_workspace_size(8, 4096, 1536, 16)
     assert 0 < a < b
-    assert L.mwc_ssm_fwd_workspace_size(8, 2048, 1536, 16) == 8 * 2048 * 32 * 4
+    assert L.mwc_ssm_fwd_workspace_size(8, 2048, 1536, 16) == 0  # the forward stages through LDS
     assert L.mwc_pscan_workspace_size(4, 65536, 1024) > 0
 
 
