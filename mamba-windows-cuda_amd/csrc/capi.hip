@@ -58,11 +58,12 @@ int mwc_set_hip_error(hipError_t e, const char* what) {
 
 namespace mwc {
 
+// States per lane. Measured on MI355X at B=8, L=2048, D=1536 (fp16): SPL=2 (8 lanes per
+// channel, 1.5 waves per SIMD) beats SPL=4 (one wave per SIMD, every stall exposed) and SPL=1
+// (4x the per-lane overhead). Small problems use SPL=1 for parallelism.
 int choose_spl(int64_t channels) {
     if (const int o = spl_override()) return o;
-    if (channels >= 8192) return 4;
-    if (channels >= 2048) return 2;
-    return 1;
+    return channels >= 2048 ? 2 : 1;
 }
 
 size_t fwd_workspace_bytes(const SsmShape& s) {

@@ -27,6 +27,8 @@
 // partial, which a second small kernel sums in fixed order (deterministic, no
 // atomics). dA and dD accumulate in registers over t and are summed over b by
 // the finishing kernel.
+#include <type_traits>
+
 #include "common.h"
 #include "launch.h"
 
@@ -35,7 +37,6 @@ namespace mwc {
 namespace {
 
 constexpr int kRedSlots = 4;  // steps folded per in-wave LDS reduction
-constexpr int kRowPad = 36;   // floats per channel row of the slab (16 g + 16 h + pad)
 
 template <int K>
 __device__ __forceinline__ void ldv(const float* p, float (&v)[K]) {
@@ -80,7 +81,7 @@ __device__ __forceinline__ void wave_lds_fence() {
 }  // namespace
 
 template <typename T, int SPL>
-__global__ void __launch_bounds__(256) ssm_bwd_kernel(
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) ssm_bwd_kernel(
     const T* __restrict__ u, const T* __restrict__ delta, const T* __restrict__ A, const T* __restrict__ Bm,
     const T* __restrict__ Cm, const T* __restrict__ Dv, const T* __restrict__ dout, const T* __restrict__ dh_last,
     const float* __restrict__ ckpt, T* __restrict__ du, T* __restrict__ ddelta, T* __restrict__ dh_prev,
@@ -97,11 +98,19 @@ __global__ void __launch_bounds__(256) ssm_bwd_kernel(
     constexpr int HALF = CPW / 2;  // channels each folding lane sums
     static_assert(NSG * SPG == TC && CPW >= 2, "tiling");
 
-    __shared__ float s_in[2][4][CPB][RS];  // [buf][delta, delta*u, u, dout][channel][step]
+    // [buf][delta, delta*u, u, dout] planes of [channel][step]; planes are AS floats apart
+    // (AS = 16 mod 64 banks) so the delta*u and dout weights of one channel sit in different banks
+    constexpr int AS = CPB * RS + 16;
+    __shared__ float s_in_raw[2][4 * AS];
     __shared__ float s_bc[2][TC][2 * kNState];
-    __shared__ float s_red[4][kRedSlots][CPW][kRowPad];
-    __shared__ float s_part[2][4][TC][2 * kNState];
-    __shared__ float s_out[2][2][TC][OS];  // [buf][du, ddelta][step][channel]
+    // wave-private slabs of g_t (plane 0) and h_t (plane 1): [wave][plane][half][slot][channel][16];
+    // a 16-lane group deposits 64 consecutive floats, plane 1 is offset by 32 banks
+    constexpr int SLAB = 2 * kRedSlots * CPW * kNState + 32;
+    __shared__ float s_red[4][2 * SLAB];
+    auto s_in = [&](int buf, int plane, int ch) -> float* { return &s_in_raw[buf][plane * AS + ch * RS]; };
+    // single-buffered: a second barrier after the store phase protects them
+    __shared__ float s_part[4][TC][2 * kNState];
+    __shared__ float s_out[2][TC][OS];  // [du, ddelta][step][channel]
 
     const int tid = threadIdx.x;
     const int lid = xcd_remap(blockIdx.x, gridDim.x);
@@ -164,10 +173,10 @@ __global__ void __launch_bounds__(256) ssm_bwd_kernel(
             vy[s] = ok ? static_cast<float>(py[s]) : 0.f;
             vdu[s] = vd[s] * vu[s];
         }
-        stv<SPG>(&s_in[buf][0][lc][sg * SPG], vd);
-        stv<SPG>(&s_in[buf][1][lc][sg * SPG], vdu);
-        stv<SPG>(&s_in[buf][2][lc][sg * SPG], vu);
-        stv<SPG>(&s_in[buf][3][lc][sg * SPG], vy);
+        stv<SPG>((s_in(buf, 0, lc) + sg * SPG), vd);
+        stv<SPG>((s_in(buf, 1, lc) + sg * SPG), vdu);
+        stv<SPG>((s_in(buf, 2, lc) + sg * SPG), vu);
+        stv<SPG>((s_in(buf, 3, lc) + sg * SPG), vy);
         s_bc[buf][bc_t][bc_n] = static_cast<float>(pb);
         s_bc[buf][bc_t][kNState + bc_n] = static_cast<float>(pc);
     };
@@ -181,7 +190,11 @@ __global__ void __launch_bounds__(256) ssm_bwd_kernel(
     }
     __syncthreads();
 
-    float(*red)[CPW][kRowPad] = s_red[wave];
+    float* red_g = &s_red[wave][0];     // [half][slot][channel][16]
+    float* red_h = &s_red[wave][SLAB];  // [half][slot][channel][16]
+    float amax2 = 0.f;
+#pragma unroll
+    for (int j = 0; j < SPL; ++j) amax2 = __builtin_fmaxf(amax2, __builtin_fabsf(A2[j]));
 
     for (int k = nck - 1; k >= 0; --k) {
         const int buf = k & 1;
@@ -192,35 +205,90 @@ __global__ void __launch_bounds__(256) ssm_bwd_kernel(
         float H[TC][SPL], E[TC][SPL], dt[TC];
         {
             float dtu[TC];
-            ldv<TC>(&s_in[buf][0][c][0], dt);
-            ldv<TC>(&s_in[buf][1][c][0], dtu);
-            float hh[SPL];
+            ldv<TC>(s_in(buf, 0, c), dt);
+            ldv<TC>(s_in(buf, 1, c), dtu);
+            float dmax = 0.f;
 #pragma unroll
-            for (int j = 0; j < SPL; ++j) hh[j] = hin[j];
+            for (int i = 0; i < TC; ++i) dmax = __builtin_fmaxf(dmax, __builtin_fabsf(dt[i]));
+            const bool need_clamp = __builtin_amdgcn_ballot_w64(dmax * amax2 > kExp2Clamp) != 0;
+            auto recompute = [&](auto clamp_tag) {
+                constexpr bool CLAMP = decltype(clamp_tag)::value;
+                float hh[SPL];
 #pragma unroll
-            for (int i = 0; i < TC; ++i) {
-                float Bv[SPL];
-                ldv<SPL>(&s_bc[buf][i][n0], Bv);
+                for (int j = 0; j < SPL; ++j) hh[j] = hin[j];
 #pragma unroll
-                for (int j = 0; j < SPL; ++j) {
-                    E[i][j] = exp2_clamped(dt[i] * A2[j]);
-                    hh[j] = __builtin_fmaf(E[i][j], hh[j], dtu[i] * Bv[j]);
-                    H[i][j] = hh[j];
+                for (int i = 0; i < TC; ++i) {
+                    float Bv[SPL];
+                    ldv<SPL>(&s_bc[buf][i][n0], Bv);
+#pragma unroll
+                    for (int j = 0; j < SPL; ++j) {
+                        const float x = dt[i] * A2[j];
+                        E[i][j] = CLAMP ? exp2_clamped(x) : __builtin_amdgcn_exp2f(x);
+                        hh[j] = __builtin_fmaf(E[i][j], hh[j], dtu[i] * Bv[j]);
+                        H[i][j] = hh[j];
+                    }
                 }
-            }
+            };
+            if (need_clamp)
+                recompute(std::true_type{});
+            else
+                recompute(std::false_type{});
         }
         // ---- reverse sweep ----
-        float uq[4], yq[4];
+        // LDS operands are read one step (B, C) or one 4-step group (u, dout) ahead of use,
+        // and the channel fold of a 4-step phase runs one phase later from the other half
+        // of the double-buffered slab, so no LDS read waits on a just-issued access.
+        auto fold = [&](int phase) {
+            const float* base_g = red_g + (phase & 1) * (kRedSlots * CPW * kNState);
+            const float* base_h = red_h + (phase & 1) * (kRedSlots * CPW * kNState);
+            const bool is_c = rq >= 4;
+            const float* plane = is_c ? base_h : base_g;
+            const float* wrow = s_in(buf, is_c ? 3 : 1, wave * CPW) + phase * kRedSlots + rs;
+            const int q4 = (rq & 3) * 4;
+            float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int m = 0; m < HALF; ++m) {
+                const int ch = 2 * m + rhalf;  // the two lanes of a pair take alternate channels
+                float v4[4];
+                ldv<4>(plane + (rs * CPW + ch) * kNState + q4, v4);
+                const float wgt = wrow[ch * RS];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) acc[q] = __builtin_fmaf(v4[q], wgt, acc[q]);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc[q] += dpp<kDppXor1>(acc[q]);
+            if (rhalf == 0) stv<4>(&s_part[wave][phase * kRedSlots + rs][rq * 4], acc);
+        };
+        float uq[4], yq[4], uqn[4], yqn[4], Bn[SPL], Cn[SPL];
+        ldv<4>(s_in(buf, 2, c) + TC - 4, uqn);
+        ldv<4>(s_in(buf, 3, c) + TC - 4, yqn);
+        ldv<SPL>(&s_bc[buf][TC - 1][n0], Bn);
+        ldv<SPL>(&s_bc[buf][TC - 1][kNState + n0], Cn);
 #pragma unroll
         for (int i = TC - 1; i >= 0; --i) {
-            if (i % 4 == 3) {
-                ldv<4>(&s_in[buf][2][c][i - 3], uq);
-                ldv<4>(&s_in[buf][3][c][i - 3], yq);
+            const int slot = i % kRedSlots, phase = i / kRedSlots;
+            if (slot == kRedSlots - 1) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    uq[q] = uqn[q];
+                    yq[q] = yqn[q];
+                }
+                if (i >= 4) {
+                    ldv<4>(s_in(buf, 2, c) + i - 7, uqn);
+                    ldv<4>(s_in(buf, 3, c) + i - 7, yqn);
+                }
             }
-            const float ui = uq[i % 4], yo = yq[i % 4];
             float Bv[SPL], Cv[SPL];
-            ldv<SPL>(&s_bc[buf][i][n0], Bv);
-            ldv<SPL>(&s_bc[buf][i][kNState + n0], Cv);
+#pragma unroll
+            for (int j = 0; j < SPL; ++j) {
+                Bv[j] = Bn[j];
+                Cv[j] = Cn[j];
+            }
+            if (i > 0) {
+                ldv<SPL>(&s_bc[buf][i > 0 ? i - 1 : 0][n0], Bn);
+                ldv<SPL>(&s_bc[buf][i > 0 ? i - 1 : 0][kNState + n0], Cn);
+            }
+            const float ui = uq[slot], yo = yq[slot];
             float gt[SPL];
             float r1 = 0.f, r2 = 0.f;
 #pragma unroll
@@ -236,33 +304,20 @@ __global__ void __launch_bounds__(256) ssm_bwd_kernel(
             r1 = group_sum<LPC>(r1);
             r2 = group_sum<LPC>(r2);
             // every lane of the group holds the sums; duplicate LDS writes are identical
-            s_out[buf][0][i][c] = __builtin_fmaf(Dd, yo, dt[i] * r1);
-            s_out[buf][1][i][c] = __builtin_fmaf(ui, r1, r2);
+            s_out[0][i][c] = __builtin_fmaf(Dd, yo, dt[i] * r1);
+            s_out[1][i][c] = __builtin_fmaf(ui, r1, r2);
             dDacc = __builtin_fmaf(yo, ui, dDacc);
-            const int slot = i % kRedSlots;
-            stv<SPL>(&red[slot][cw][n0], gt);
-            stv<SPL>(&red[slot][cw][kNState + n0], H[i]);
-            if (slot == 0) {
+            const int sl = ((phase & 1) * kRedSlots + slot) * CPW + cw;
+            stv<SPL>(red_g + sl * kNState + n0, gt);
+            stv<SPL>(red_h + sl * kNState + n0, H[i]);
+            if (slot == 0 && phase + 1 < TC / kRedSlots) {
                 wave_lds_fence();
-                // fold this wave's channels for steps i..i+3: weight delta*u (dB) or dout (dC)
-                const int wsel = rq < 4 ? 1 : 3;
-                const float* wrow = &s_in[buf][wsel][wave * CPW][i + rs];
-                float acc[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int m = 0; m < HALF; ++m) {
-                    const int ch = rhalf * HALF + m;
-                    float v4[4];
-                    ldv<4>(&red[rs][ch][rq * 4], v4);
-                    const float wgt = wrow[ch * RS];
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) acc[q] = __builtin_fmaf(v4[q], wgt, acc[q]);
-                }
-#pragma unroll
-                for (int q = 0; q < 4; ++q) acc[q] += dpp<kDppXor1>(acc[q]);
-                if (rhalf == 0) stv<4>(&s_part[buf][wave][i + rs][rq * 4], acc);
-                wave_lds_fence();
+                fold(phase + 1);
             }
         }
+        wave_lds_fence();
+        fold(0);
+        wave_lds_fence();
         if (k > 0) {
             commit(k - 1, buf ^ 1);
 #pragma unroll
@@ -276,8 +331,8 @@ __global__ void __launch_bounds__(256) ssm_bwd_kernel(
             const int t = t0 + st_;
             if (t < L) {
                 float a[VPT], bb[VPT];
-                ldv<VPT>(&s_out[buf][0][st_][cq], a);
-                ldv<VPT>(&s_out[buf][1][st_][cq], bb);
+                ldv<VPT>(&s_out[0][st_][cq], a);
+                ldv<VPT>(&s_out[1][st_][cq], bb);
                 T* pdu = du + (row0 + t) * D + d0 + cq;
                 T* pdd = ddelta + (row0 + t) * D + d0 + cq;
 #pragma unroll
@@ -291,10 +346,10 @@ __global__ void __launch_bounds__(256) ssm_bwd_kernel(
         // this workgroup's dB/dC partial for the chunk (sum of its 4 waves)
         for (int o = tid; o < TC * 2 * kNState; o += 256) {
             const int tt = o >> 5, v = o & 31;
-            const float s = s_part[buf][0][tt][v] + s_part[buf][1][tt][v] + s_part[buf][2][tt][v] +
-                            s_part[buf][3][tt][v];
+            const float s = s_part[0][tt][v] + s_part[1][tt][v] + s_part[2][tt][v] + s_part[3][tt][v];
             if (t0 + tt < L) dbc_part[(((int64_t)blk * Bsz + b) * L + t0 + tt) * 32 + v] = s;
         }
+        __syncthreads();  // s_out / s_part are rewritten by the next chunk
     }
 
     if (valid) {

@@ -21,6 +21,8 @@
 // loop carries no bounds checks. With at most one wave per SIMD at the target
 // shapes every issued instruction costs the wave 4 cycles, so the design
 // minimises instructions per state, not just VALU work.
+#include <type_traits>
+
 #include "common.h"
 #include "launch.h"
 
@@ -60,7 +62,7 @@ __device__ __forceinline__ void vst(float* p, const float (&v)[K]) {
 }
 
 template <typename T, int SPL, bool HAS_OUT>
-__global__ void __launch_bounds__(256) ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta,
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta,
                                                       const T* __restrict__ A, const T* __restrict__ Bm,
                                                       const T* __restrict__ Cm, const T* __restrict__ Dv,
                                                       const T* __restrict__ h_prev, T* __restrict__ out,
@@ -107,6 +109,9 @@ __global__ void __launch_bounds__(256) ssm_fwd_kernel(const T* __restrict__ u, c
         h[j] = h_prev ? ld(h_prev + ((int64_t)b * D + d) * kNState + n0 + j) : 0.f;
     }
     const float Dd = ld(Dv + d);
+    float amax2 = 0.f;  // max_j |A_j| * log2(e) over this lane's states
+#pragma unroll
+    for (int j = 0; j < SPL; ++j) amax2 = __builtin_fmaxf(amax2, __builtin_fabsf(A2[j]));
 
     T pu[SPG], pd[SPG], pb, pc;
     auto issue = [&](int k) {
@@ -150,28 +155,44 @@ __global__ void __launch_bounds__(256) ssm_fwd_kernel(const T* __restrict__ u, c
         if (more) issue(k + 1);
         if (ckb != nullptr && valid) vst<SPL>(ckb + (int64_t)k * D * kNState, h);
 
-        float dt[TC], dtu[TC], uu[TC];
+        // the whole chunk's operands, read up front so LDS latency is paid once per chunk
+        float dt[TC], dtu[TC], uu[TC], Bv[TC][SPL], Cv[TC][SPL];
         lds_ld<TC>(&s_in[buf][0][c][0], dt);
         lds_ld<TC>(&s_in[buf][1][c][0], dtu);
         if constexpr (HAS_OUT) lds_ld<TC>(&s_in[buf][2][c][0], uu);
 #pragma unroll
         for (int i = 0; i < TC; ++i) {
-            float Bv[SPL], Cv[SPL];
-            lds_ld<SPL>(&s_bc[buf][i][n0], Bv);
-            if constexpr (HAS_OUT) lds_ld<SPL>(&s_bc[buf][i][kNState + n0], Cv);
-            float y = 0.f;
-#pragma unroll
-            for (int j = 0; j < SPL; ++j) {
-                const float e = exp2_clamped(dt[i] * A2[j]);
-                h[j] = __builtin_fmaf(e, h[j], dtu[i] * Bv[j]);
-                if constexpr (HAS_OUT) y = __builtin_fmaf(Cv[j], h[j], y);
-            }
-            if constexpr (HAS_OUT) {
-                y = group_sum<LPC>(y);
-                // every lane of the group holds the sum; the duplicate LDS writes are identical
-                s_y[buf][i][c] = __builtin_fmaf(Dd, uu[i], y);
-            }
+            lds_ld<SPL>(&s_bc[buf][i][n0], Bv[i]);
+            if constexpr (HAS_OUT) lds_ld<SPL>(&s_bc[buf][i][kNState + n0], Cv[i]);
         }
+        // |delta*A| <= 88 for the whole chunk (the usual case) -> no clamp needed
+        float dmax = 0.f;
+#pragma unroll
+        for (int i = 0; i < TC; ++i) dmax = __builtin_fmaxf(dmax, __builtin_fabsf(dt[i]));
+        const bool need_clamp = __builtin_amdgcn_ballot_w64(dmax * amax2 > kExp2Clamp) != 0;
+        auto run = [&](auto clamp_tag) {
+            constexpr bool CLAMP = decltype(clamp_tag)::value;
+#pragma unroll
+            for (int i = 0; i < TC; ++i) {
+                float y = 0.f;
+#pragma unroll
+                for (int j = 0; j < SPL; ++j) {
+                    const float x = dt[i] * A2[j];
+                    const float e = CLAMP ? exp2_clamped(x) : __builtin_amdgcn_exp2f(x);
+                    h[j] = __builtin_fmaf(e, h[j], dtu[i] * Bv[i][j]);
+                    if constexpr (HAS_OUT) y = __builtin_fmaf(Cv[i][j], h[j], y);
+                }
+                if constexpr (HAS_OUT) {
+                    y = group_sum<LPC>(y);
+                    // every lane of the group holds the sum; the duplicate LDS writes are identical
+                    s_y[buf][i][c] = __builtin_fmaf(Dd, uu[i], y);
+                }
+            }
+        };
+        if (need_clamp)
+            run(std::true_type{});
+        else
+            run(std::false_type{});
         if (more) commit(k + 1, buf ^ 1);
         __syncthreads();
         if constexpr (HAS_OUT) {
