@@ -220,6 +220,31 @@ def cpu_baseline(cfg, d_frac=2):
                       f"os.cpu_count()={os.cpu_count()}, affinity={cores}"}
 
 
+def kernels_only(cfg):
+    """Profiling driver: three fused forward/backward calls at `cfg`, three cfg4b scans and a
+    1 GiB device copy (the copy calibrates rocprofv3's FETCH_SIZE/WRITE_SIZE counters)."""
+    import torch
+
+    from mamba_windows_cuda import ops, parallel_scan_fn, workloads
+
+    x = workloads.config_inputs(cfg, device="cuda", gen_device="cuda")
+    for _ in range(3):
+        _, _, ck = ops.ssm_forward(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], want_ckpt=True,
+                                   want_h_last=False)
+        ops.ssm_backward(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["dout"], ck)
+    del x
+    a, b = workloads.pscan_inputs(device="cuda", gen_device="cuda")
+    for _ in range(3):
+        parallel_scan_fn(a, b)
+    del a, b
+    src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return {"mode": "kernels-only", "config": cfg, "calibration_copy_bytes": src.numel() * 4}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -228,6 +253,8 @@ def main():
     ap.add_argument("--config", default="cfg2", choices=["cfg2", "cfg3", "cfg4a", "cfg4b"])
     ap.add_argument("--level", type=int, default=0, choices=[0, 1])
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--kernels-only", action="store_true",
+                    help="profiling driver: fused calls, cfg4b scan and a 1 GiB copy; no timing")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build measures one GPU only; multi-GPU sharding is design-only "
@@ -238,6 +265,9 @@ def main():
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no HIP device visible"}))
         sys.exit(1)
+    if args.kernels_only:
+        print(json.dumps(kernels_only(args.config if args.config in ("cfg2", "cfg3") else "cfg2")))
+        return
     if args.config == "cfg4b":
         res = bench_pscan(args.steps, args.warmup)
     elif args.config == "cfg4a":
