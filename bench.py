@@ -80,6 +80,13 @@ def bench_ssm(cfg, steps, warmup, level):
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
+    # activation memory a forward keeps for its backward at this checkpoint level
+    base = torch.cuda.memory_allocated()
+    out_keep = m(leaves["u"], leaves["delta"], leaves["A"], leaves["B"], leaves["C"], leaves["D"])
+    torch.cuda.synchronize()
+    kept = torch.cuda.memory_allocated() - base - out_keep.numel() * out_keep.element_size()
+    del out_keep
+    torch.cuda.reset_peak_memory_stats()
     t0 = time.perf_counter()
     ms_events = _events_ms(step, steps)
     torch.cuda.synchronize()
@@ -125,6 +132,7 @@ def bench_ssm(cfg, steps, warmup, level):
         "step_hbm": {"algorithmic_bytes": bytes_fwd + bytes_bwd, "achieved_GBps": gbs_step,
                      "frac_of_peak": gbs_step / HBM_PEAK_GBS},
         "wall_ms_per_step": wall_ms,
+        "retained_after_forward_GB": kept / 1e9,
     }
     return res
 

@@ -66,15 +66,25 @@ int choose_spl(int64_t channels) {
     return channels >= 2048 ? 2 : 1;
 }
 
+// Kernel family: 2 = lane groups (ssm_fwd.hip / ssm_bwd.hip, the default), 3 = state groups across
+// waves (ssm_v3.hip; selectable with MWC_IMPL=3 while it is slower at the benchmark shapes).
+int impl_choice() {
+    static const int v = [] {
+        const char* e = getenv("MWC_IMPL");
+        return (e && atoi(e) == 3) ? 3 : 2;
+    }();
+    return v;
+}
+
 size_t fwd_workspace_bytes(const SsmShape& s) {
-    (void)s;
-    return 0;  // the forward stages its inputs through LDS and needs no scratch
+    // the state-group kernels read a packed fp32 copy of B/C; the lane-group kernels need nothing
+    return impl_choice() == 3 ? v3_bcp_bytes(s) : 0;
 }
 
 size_t bwd_workspace_bytes(const SsmShape& s) {
-    const int spl = choose_spl(s.batch * s.dim);
-    const int ngrp = bwd_groups(s, spl);
-    size_t n = align256((size_t)ngrp * s.batch * s.seqlen * 32 * sizeof(float));  // dB/dC partials
+    const int ngrp = impl_choice() == 3 ? v3_groups(s) : bwd_groups(s, choose_spl(s.batch * s.dim));
+    size_t n = fwd_workspace_bytes(s);
+    n += align256((size_t)ngrp * s.batch * s.seqlen * 32 * sizeof(float));  // dB/dC partials
     n += align256((size_t)s.batch * s.dim * kNState * sizeof(float));         // dA partials
     n += align256((size_t)s.batch * s.dim * sizeof(float));                   // dD partials
     return n;
@@ -124,10 +134,18 @@ int mwc_ssm_fwd(int dtype, const void* u, const void* delta, const void* A, cons
     if (seqlen > 0 && (!u || !delta || !B_ssm || !C_ssm))
         return fail(MWC_ERR_INVALID_ARGUMENT, "u, delta, B_ssm and C_ssm must not be NULL");
     const mwc::SsmShape s{batch, seqlen, dim};
-    (void)workspace;
-    (void)workspace_bytes;
     const bool half = dtype == MWC_DTYPE_F16;
     hipStream_t st = (hipStream_t)stream;
+    if (mwc::impl_choice() == 3) {
+        const size_t need = mwc::fwd_workspace_bytes(s);
+        if (seqlen > 0 && (workspace == nullptr || workspace_bytes < need))
+            return fail(MWC_ERR_WORKSPACE, "forward workspace too small: need %zu bytes, got %zu", need,
+                        workspace_bytes);
+        float* bcp = (float*)workspace;
+        if (seqlen > 0) MWC_HIP_TRY(mwc::launch_v3_pack(half, B_ssm, C_ssm, bcp, s, st));
+        MWC_HIP_TRY(mwc::launch_v3_fwd(half, u, delta, A, bcp, D_ssm, h_prev, out, h_last, ckpt, s, st));
+        return MWC_OK;
+    }
     const int spl = mwc::choose_spl(batch * dim);
     MWC_HIP_TRY(mwc::launch_ssm_fwd(half, spl, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, out, h_last, ckpt, s, st));
     return MWC_OK;
@@ -152,16 +170,25 @@ int mwc_ssm_bwd(int dtype, const void* u, const void* delta, const void* A, cons
         return fail(MWC_ERR_WORKSPACE, "backward workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
     const bool half = dtype == MWC_DTYPE_F16;
     hipStream_t st = (hipStream_t)stream;
+    const bool v3 = mwc::impl_choice() == 3;
     const int spl = mwc::choose_spl(batch * dim);
-    const int ngrp = mwc::bwd_groups(s, spl);
+    const int ngrp = v3 ? mwc::v3_groups(s) : mwc::bwd_groups(s, spl);
     char* w = (char*)workspace;
+    float* bcp = (float*)w;
+    w += mwc::fwd_workspace_bytes(s);
     float* dbc_part = (float*)w;
     w += align256((size_t)ngrp * batch * seqlen * 32 * sizeof(float));
     float* dA_part = (float*)w;
     w += align256((size_t)batch * dim * mwc::kNState * sizeof(float));
     float* dD_part = (float*)w;
-    MWC_HIP_TRY(mwc::launch_ssm_bwd(half, spl, u, delta, A, B_ssm, C_ssm, D_ssm, dout, dh_last, ckpt, du, ddelta, dh_prev,
-                                    dA_part, dD_part, dbc_part, s, st));
+    if (v3) {
+        if (seqlen > 0) MWC_HIP_TRY(mwc::launch_v3_pack(half, B_ssm, C_ssm, bcp, s, st));
+        MWC_HIP_TRY(mwc::launch_v3_bwd(half, u, delta, A, bcp, D_ssm, dout, dh_last, ckpt, du, ddelta, dh_prev,
+                                       dA_part, dD_part, dbc_part, s, st));
+    } else {
+        MWC_HIP_TRY(mwc::launch_ssm_bwd(half, spl, u, delta, A, B_ssm, C_ssm, D_ssm, dout, dh_last, ckpt, du,
+                                        ddelta, dh_prev, dA_part, dD_part, dbc_part, s, st));
+    }
     MWC_HIP_TRY(mwc::launch_bwd_finish(half, dbc_part, dA_part, dD_part, dB, dC, dA, dD, ngrp, s, st));
     return MWC_OK;
 }

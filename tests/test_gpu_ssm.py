@@ -197,3 +197,68 @@ def test_no_grad_forward_keeps_nothing(dev):
         out = m(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"])
     torch.cuda.synchronize()
     assert torch.cuda.memory_allocated() - base <= out.numel() * out.element_size() + 4096
+
+
+def _retained_after_forward(x, dev, lvl):
+    """Device bytes a forward keeps alive for its backward (inputs excluded)."""
+    leaves = {k: v.to(dev).requires_grad_(k != "dout") for k, v in x.items()}
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated()
+    out = SelectiveScanCuda(checkpoint_lvl=lvl)(leaves["u"], leaves["delta"], leaves["A"], leaves["B"],
+                                                leaves["C"], leaves["D"])
+    torch.cuda.synchronize()
+    kept = torch.cuda.memory_allocated() - before - out.numel() * out.element_size()
+    del out
+    return kept
+
+
+def test_config3_training_step_both_levels(dev):
+    """Mamba-2.8B layer shape, fp16 (B=4, L=4096, D=5120): checkpoint levels 0 and 1 give
+    bitwise-equal results, level 1 keeps nothing between forward and backward while level 0
+    keeps the fp32 state every 16 steps, and both match the float64 oracle."""
+    x = workloads.config_inputs("cfg3")
+    B, L, D = 4, 4096, 5120
+    kept0 = _retained_after_forward(x, dev, 0)
+    kept1 = _retained_after_forward(x, dev, 1)
+    assert kept0 >= B * ((L + 15) // 16) * D * 16 * 4
+    assert kept1 < kept0 // 100
+    print("case cfg3 level 0", flush=True)
+    out0, _, g0 = _run(x, dev, with_h=False, lvl=0)
+    print("case cfg3 level 1", flush=True)
+    out1, _, g1 = _run(x, dev, with_h=False, lvl=1)
+    assert torch.equal(out0, out1)
+    for k in g0:
+        assert torch.equal(g0[k], g1[k]), k
+    del out1, g1
+    print("case cfg3 oracle", flush=True)
+    ro, _ = orc.ssm_fwd(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], None, clamp=True)
+    _close("out", out0, ro, torch.float16)
+    del ro
+    r = orc.ssm_bwd(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["dout"], None, None, clamp=True)
+    for k, name in GRADS:
+        _close(name, g0[k], r[name], torch.float16)
+
+
+def test_config4a_streaming_long_sequence(dev):
+    """fp32, B=1, L=131072, D=2048 fed as 32 chunks of 4096 through forward_with_state:
+    h_last equals one full-length pass, and out/h_last match the float64 oracle on a
+    256-channel slice (channels are independent in the forward)."""
+    x = workloads.config_inputs("cfg4a", dout=False)
+    xd = {k: v.to(dev) for k, v in x.items()}
+    m = SelectiveScanCuda()
+    with torch.no_grad():
+        h = None
+        outs = []
+        for s0 in range(0, 131072, 4096):
+            sl = slice(s0, s0 + 4096)
+            o, h = m.forward_with_state(xd["u"][:, sl], xd["delta"][:, sl], xd["A"], xd["B"][:, sl],
+                                        xd["C"][:, sl], xd["D"], h)
+            outs.append(o[:, :, :256].cpu())
+        full_out, full_h = m.forward_with_state(xd["u"], xd["delta"], xd["A"], xd["B"], xd["C"], xd["D"])
+    torch.cuda.synchronize()
+    torch.testing.assert_close(h, full_h, rtol=1e-5, atol=1e-6)
+    ro, rh = orc.ssm_fwd(x["u"][:, :, :256], x["delta"][:, :, :256], x["A"][:256], x["B"], x["C"],
+                         x["D"][:256], None, clamp=True)
+    _close("h_last", h[:, :256], rh, torch.float32)
+    _close("out", torch.cat(outs, 1), ro, torch.float32)
+    _close("out_full", full_out[:, :, :256], ro, torch.float32)
