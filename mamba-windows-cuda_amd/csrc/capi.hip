@@ -18,13 +18,10 @@ thread_local char g_err[512] = "";
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 int spl_override() {
-    static const int v = [] {
-        const char* e = getenv("MWC_SPL");
-        if (!e) return 0;
-        const int s = atoi(e);
-        return (s == 1 || s == 2 || s == 4) ? s : 0;
-    }();
-    return v;
+    const char* e = getenv("MWC_SPL");
+    if (!e) return 0;
+    const int s = atoi(e);
+    return (s == 1 || s == 2 || s == 4) ? s : 0;
 }
 
 int fail(int status, const char* fmt, ...) {
@@ -59,11 +56,93 @@ int mwc_set_hip_error(hipError_t e, const char* what) {
 namespace mwc {
 
 // States per lane. Measured on MI355X at B=8, L=2048, D=1536 (fp16): SPL=2 (8 lanes per
-// channel, 1.5 waves per SIMD) beats SPL=4 (one wave per SIMD, every stall exposed) and SPL=1
-// (4x the per-lane overhead). Small problems use SPL=1 for parallelism.
+// channel) beats SPL=4 (one wave per SIMD, every stall exposed) and SPL=1 (4x the per-lane
+// overhead of the n-reductions). Small problems use SPL=1 for parallelism.
 int choose_spl(int64_t channels) {
     if (const int o = spl_override()) return o;
     return channels >= 2048 ? 2 : 1;
+}
+
+namespace {
+
+constexpr int kCUs = 256;  // MI355X compute units (4 SIMDs each); a workgroup is 4 waves on one CU
+
+int env_int(const char* name, int lo, int hi) {
+    const char* e = getenv(name);
+    if (!e) return 0;
+    const int v = atoi(e);
+    return (v >= lo && v <= hi) ? v : 0;
+}
+
+// Relative throughput of a SIMD running q of these (issue- and latency-bound) waves at once.
+double simd_throughput(int64_t q) {
+    static const double t[] = {0.0, 1.0, 1.7, 2.2, 2.5};
+    return q < 5 ? t[q] : 2.6;
+}
+
+// Duration, in units of one chunk of one lone wave, of a pass of `wgs` equal workgroups of
+// `chunks` chunks each when a CU holds at most `cap` of them at once.
+double pass_time(int64_t wgs, int64_t chunks, int cap) {
+    if (wgs <= 0 || chunks <= 0) return 0.0;
+    const int64_t m = (wgs + kCUs - 1) / kCUs;  // workgroups on the busiest CU
+    const int64_t r = (m + cap - 1) / cap;      // rounds
+    const int64_t q = (m + r - 1) / r;          // workgroups per CU in a round
+    return (double)r * ((double)chunks * q / simd_throughput(q) + 1.0);  // +1: prologue, first loads
+}
+
+int cpb_of(int spl) { return 4 * 64 / (kNState / spl); }
+
+// Picks the segment count (and the carry split) minimising the modelled time of
+// carry pass + main pass. caps = workgroups per CU each kernel fits (registers, LDS);
+// carry_rel = cost of a carry-pass chunk relative to a main-pass chunk.
+SegPlan plan(const SsmShape& s, bool bwd, int cap_main, int cap_carry, double carry_rel) {
+    const int spl = choose_spl(s.batch * s.dim);
+    const int64_t nck = (s.seqlen + kCkptSteps - 1) / kCkptSteps;
+    const int64_t w1 = s.batch * ((s.dim + cpb_of(spl) - 1) / cpb_of(spl));
+    SegPlan best{spl, 1, (int)nck, 1, 0};
+    double best_t = pass_time(w1, nck, cap_main);
+    // MWC_NSEG / MWC_CFOLD force the segment count / carry split (tuning and tests)
+    const int force_n = env_int("MWC_NSEG", 1, 1 << 20), force_f = env_int("MWC_CFOLD", 1, 64);
+    if (force_n == 1 || nck < 2) return best;
+    const int n_lo = force_n ? force_n : 2, n_hi = force_n ? force_n : 16;
+    for (int n = n_lo; n <= n_hi; ++n) {
+        for (int f = force_f ? force_f : 1; f <= (force_f ? force_f : 8); f *= 2) {
+            const int64_t cps = ((nck + n - 1) / n + f - 1) / f * f;  // chunks per segment, a multiple of f
+            const int64_t nseg = (nck + cps - 1) / cps;                 // non-empty segments
+            if (nseg < 2) continue;
+            const int64_t ccps = cps / f;
+            const int64_t ncar = bwd ? (nck - cps + ccps - 1) / ccps : (nseg - 1) * f;
+            const double t = pass_time(w1 * nseg, cps, cap_main) + carry_rel * pass_time(w1 * ncar, ccps, cap_carry);
+            if (t < best_t * 0.98 || force_n) {
+                best_t = t;
+                best = SegPlan{spl, (int)nseg, (int)cps, f, (int)ncar};
+            }
+        }
+    }
+    return best;
+}
+
+// Workgroups per CU each kernel fits, by SPL: min(512 / VGPRs per lane, 160 KB / LDS per
+// workgroup), from the gfx950 build's resource usage.
+int fwd_cap(int spl) { return spl == 1 ? 4 : spl == 2 ? 3 : 1; }
+int fwd_carry_cap(int spl) { return spl == 1 ? 5 : spl == 2 ? 4 : 2; }
+int bwd_cap(int spl) { return spl == 1 ? 3 : spl == 2 ? bwd_min_waves(2) : 1; }
+int bwd_carry_cap(int spl) { return spl == 1 ? 5 : spl == 2 ? 4 : 2; }
+
+size_t carry_bytes(const SsmShape& s, const SegPlan& p) {
+    return p.nseg > 1 ? align256((size_t)s.batch * p.ncar * s.dim * kNState * sizeof(float)) : 0;
+}
+
+}  // namespace
+
+SegPlan plan_fwd(const SsmShape& s) {
+    const int spl = choose_spl(s.batch * s.dim);
+    return plan(s, false, fwd_cap(spl), fwd_carry_cap(spl), 0.6);
+}
+
+SegPlan plan_bwd(const SsmShape& s) {
+    const int spl = choose_spl(s.batch * s.dim);
+    return plan(s, true, bwd_cap(spl), bwd_carry_cap(spl), 0.3);
 }
 
 // Kernel family: 2 = lane groups (ssm_fwd.hip / ssm_bwd.hip, the default), 3 = state groups across
@@ -77,16 +156,25 @@ int impl_choice() {
 }
 
 size_t fwd_workspace_bytes(const SsmShape& s) {
-    // the state-group kernels read a packed fp32 copy of B/C; the lane-group kernels need nothing
-    return impl_choice() == 3 ? v3_bcp_bytes(s) : 0;
+    // the state-group kernels read a packed fp32 copy of B/C; the lane-group kernels need the
+    // segment carries when L is split
+    if (impl_choice() == 3) return v3_bcp_bytes(s);
+    return 2 * carry_bytes(s, plan_fwd(s));
 }
 
 size_t bwd_workspace_bytes(const SsmShape& s) {
-    const int ngrp = impl_choice() == 3 ? v3_groups(s) : bwd_groups(s, choose_spl(s.batch * s.dim));
-    size_t n = fwd_workspace_bytes(s);
-    n += align256((size_t)ngrp * s.batch * s.seqlen * 32 * sizeof(float));  // dB/dC partials
-    n += align256((size_t)s.batch * s.dim * kNState * sizeof(float));         // dA partials
-    n += align256((size_t)s.batch * s.dim * sizeof(float));                   // dD partials
+    if (impl_choice() == 3) {
+        size_t n = v3_bcp_bytes(s);
+        n += align256((size_t)v3_groups(s) * s.batch * s.seqlen * 32 * sizeof(float));
+        n += align256((size_t)s.batch * s.dim * kNState * sizeof(float));
+        n += align256((size_t)s.batch * s.dim * sizeof(float));
+        return n;
+    }
+    const SegPlan p = plan_bwd(s);
+    size_t n = align256((size_t)bwd_groups(s, p.spl) * s.batch * s.seqlen * 32 * sizeof(float));  // dB/dC
+    n += align256((size_t)p.nseg * s.batch * s.dim * kNState * sizeof(float));                      // dA
+    n += align256((size_t)p.nseg * s.batch * s.dim * sizeof(float));                                // dD
+    n += 2 * carry_bytes(s, p);
     return n;
 }
 
@@ -136,18 +224,21 @@ int mwc_ssm_fwd(int dtype, const void* u, const void* delta, const void* A, cons
     const mwc::SsmShape s{batch, seqlen, dim};
     const bool half = dtype == MWC_DTYPE_F16;
     hipStream_t st = (hipStream_t)stream;
+    const size_t need = mwc::fwd_workspace_bytes(s);
+    if (seqlen > 0 && need > 0 && (workspace == nullptr || workspace_bytes < need))
+        return fail(MWC_ERR_WORKSPACE, "forward workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
     if (mwc::impl_choice() == 3) {
-        const size_t need = mwc::fwd_workspace_bytes(s);
-        if (seqlen > 0 && (workspace == nullptr || workspace_bytes < need))
-            return fail(MWC_ERR_WORKSPACE, "forward workspace too small: need %zu bytes, got %zu", need,
-                        workspace_bytes);
         float* bcp = (float*)workspace;
         if (seqlen > 0) MWC_HIP_TRY(mwc::launch_v3_pack(half, B_ssm, C_ssm, bcp, s, st));
         MWC_HIP_TRY(mwc::launch_v3_fwd(half, u, delta, A, bcp, D_ssm, h_prev, out, h_last, ckpt, s, st));
         return MWC_OK;
     }
-    const int spl = mwc::choose_spl(batch * dim);
-    MWC_HIP_TRY(mwc::launch_ssm_fwd(half, spl, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, out, h_last, ckpt, s, st));
+    const mwc::SegPlan p = mwc::plan_fwd(s);
+    float* car_h = (float*)workspace;
+    float* car_x = (float*)((char*)workspace + need / 2);
+    const mwc::FwdArgs a{u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, out, h_last, ckpt, car_h, car_x,
+                         p.nseg, p.cps, p.cfold, p.ncar};
+    MWC_HIP_TRY(mwc::launch_ssm_fwd(half, p.spl, a, s, st));
     return MWC_OK;
 }
 
@@ -170,26 +261,38 @@ int mwc_ssm_bwd(int dtype, const void* u, const void* delta, const void* A, cons
         return fail(MWC_ERR_WORKSPACE, "backward workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
     const bool half = dtype == MWC_DTYPE_F16;
     hipStream_t st = (hipStream_t)stream;
-    const bool v3 = mwc::impl_choice() == 3;
-    const int spl = mwc::choose_spl(batch * dim);
-    const int ngrp = v3 ? mwc::v3_groups(s) : mwc::bwd_groups(s, spl);
     char* w = (char*)workspace;
-    float* bcp = (float*)w;
-    w += mwc::fwd_workspace_bytes(s);
-    float* dbc_part = (float*)w;
-    w += align256((size_t)ngrp * batch * seqlen * 32 * sizeof(float));
-    float* dA_part = (float*)w;
-    w += align256((size_t)batch * dim * mwc::kNState * sizeof(float));
-    float* dD_part = (float*)w;
-    if (v3) {
+    if (mwc::impl_choice() == 3) {
+        const int ngrp = mwc::v3_groups(s);
+        float* bcp = (float*)w;
+        w += mwc::v3_bcp_bytes(s);
+        float* dbc_part = (float*)w;
+        w += align256((size_t)ngrp * batch * seqlen * 32 * sizeof(float));
+        float* dA_part = (float*)w;
+        w += align256((size_t)batch * dim * mwc::kNState * sizeof(float));
+        float* dD_part = (float*)w;
         if (seqlen > 0) MWC_HIP_TRY(mwc::launch_v3_pack(half, B_ssm, C_ssm, bcp, s, st));
         MWC_HIP_TRY(mwc::launch_v3_bwd(half, u, delta, A, bcp, D_ssm, dout, dh_last, ckpt, du, ddelta, dh_prev,
                                        dA_part, dD_part, dbc_part, s, st));
-    } else {
-        MWC_HIP_TRY(mwc::launch_ssm_bwd(half, spl, u, delta, A, B_ssm, C_ssm, D_ssm, dout, dh_last, ckpt, du,
-                                        ddelta, dh_prev, dA_part, dD_part, dbc_part, s, st));
+        MWC_HIP_TRY(mwc::launch_bwd_finish(half, dbc_part, dA_part, dD_part, dB, dC, dA, dD, ngrp, (int)batch, s, st));
+        return MWC_OK;
     }
-    MWC_HIP_TRY(mwc::launch_bwd_finish(half, dbc_part, dA_part, dD_part, dB, dC, dA, dD, ngrp, s, st));
+    const mwc::SegPlan p = mwc::plan_bwd(s);
+    const int ngrp = mwc::bwd_groups(s, p.spl);
+    float* dbc_part = (float*)w;
+    w += align256((size_t)ngrp * batch * seqlen * 32 * sizeof(float));
+    float* dA_part = (float*)w;
+    w += align256((size_t)p.nseg * batch * dim * mwc::kNState * sizeof(float));
+    float* dD_part = (float*)w;
+    w += align256((size_t)p.nseg * batch * dim * sizeof(float));
+    float* car_g = (float*)w;
+    w += mwc::carry_bytes(s, p);
+    float* car_x = (float*)w;
+    const mwc::BwdArgs a{u, delta, A, B_ssm, C_ssm, D_ssm, dout, dh_last, ckpt, du, ddelta, dh_prev,
+                         dA_part, dD_part, dbc_part, car_g, car_x, p.nseg, p.cps, p.cfold, p.ncar};
+    MWC_HIP_TRY(mwc::launch_ssm_bwd(half, p.spl, a, s, st));
+    MWC_HIP_TRY(mwc::launch_bwd_finish(half, dbc_part, dA_part, dD_part, dB, dC, dA, dD, ngrp, p.nseg * (int)batch,
+                                       s, st));
     return MWC_OK;
 }
 

@@ -9,26 +9,55 @@ struct SsmShape {
     int64_t batch, seqlen, dim;
 };
 
-// Channel-grouping choice: SPL = states held per lane (4 lanes x 4 states per
-// channel by default). Returns 1, 2 or 4.
-int choose_spl(int64_t channels);
+// Waves per SIMD the lane-group kernels are compiled to fit (each lane then has 512/W VGPRs).
+// The backward at SPL=2 needs ~200 VGPRs for its chunk of recomputed states; squeezed to 3 waves
+// it spills (the build option MWC_BWD_SPL2_WAVES selects 2 or 3).
+#ifndef MWC_BWD_SPL2_WAVES
+#define MWC_BWD_SPL2_WAVES 2
+#endif
+constexpr int fwd_min_waves(int spl) { return spl == 4 ? 1 : 3; }
+constexpr int bwd_min_waves(int spl) { return spl == 4 ? 1 : spl == 2 ? MWC_BWD_SPL2_WAVES : 3; }
+
+// Launch plan of the lane-group kernels: SPL = states held per lane (16/SPL lanes per channel),
+// nseg = segments L is cut into (cps chunks of kCkptSteps steps each), cfold = carry segments per
+// segment (the carry passes run cps/cfold chunks per workgroup), ncar = carry segments in all.
+struct SegPlan {
+    int spl, nseg, cps, cfold, ncar;
+};
+SegPlan plan_fwd(const SsmShape& s);
+SegPlan plan_bwd(const SsmShape& s);
 
 // Workspace carve-up (bytes, 256-aligned pieces).
 size_t fwd_workspace_bytes(const SsmShape& s);
 size_t bwd_workspace_bytes(const SsmShape& s);
 int bwd_groups(const SsmShape& s, int spl);  // channel groups that write dB/dC partials
 
+struct FwdArgs {
+    const void *u, *delta, *A, *B, *C, *Dv, *h_prev;
+    void *out, *h_last;        // out == NULL: state-only pass (checkpoints and/or h_last)
+    float* ckpt;               // [batch][nck][dim][16] or NULL
+    float *car_h, *car_x;      // [batch][ncar][dim][16] carries (nseg > 1)
+    int nseg, cps, cfold, ncar;
+};
+
+struct BwdArgs {
+    const void *u, *delta, *A, *B, *C, *Dv, *dout, *dh_last;
+    const float* ckpt;
+    void *du, *ddelta, *dh_prev;
+    float* dA_part;            // [nseg][batch][dim][16]
+    float* dD_part;            // [nseg][batch][dim]
+    float* dbc_part;           // [groups][batch][seqlen][32]
+    float *car_g, *car_x;      // [batch][ncar][dim][16] adjoint carries (nseg > 1)
+    int nseg, cps, cfold, ncar;
+};
+
 // Kernel launchers; `is_half` selects fp16 storage. They only enqueue work.
-hipError_t launch_ssm_fwd(bool is_half, int spl, const void* u, const void* delta, const void* A,
-                          const void* B, const void* C, const void* Dv, const void* h_prev, void* out,
-                          void* h_last, float* ckpt, const SsmShape& s, hipStream_t st);
-hipError_t launch_ssm_bwd(bool is_half, int spl, const void* u, const void* delta, const void* A,
-                          const void* B, const void* C, const void* Dv, const void* dout, const void* dh_last,
-                          const float* ckpt, void* du, void* ddelta, void* dh_prev, float* dA_part,
-                          float* dD_part, float* dbc_part, const SsmShape& s, hipStream_t st);
+hipError_t launch_ssm_fwd(bool is_half, int spl, const FwdArgs& a, const SsmShape& s, hipStream_t st);
+hipError_t launch_ssm_bwd(bool is_half, int spl, const BwdArgs& a, const SsmShape& s, hipStream_t st);
+// Sums the dB/dC partials of `ngroups` channel groups and the dA/dD partials of `nrows` rows.
 hipError_t launch_bwd_finish(bool is_half, const float* dbc_part, const float* dA_part,
                              const float* dD_part, void* dB, void* dC, void* dA, void* dD,
-                             int ngroups, const SsmShape& s, hipStream_t st);
+                             int ngroups, int nrows, const SsmShape& s, hipStream_t st);
 
 // "state groups across waves" kernels (ssm_v3.hip)
 int impl_choice();  // 2 = lane groups (default), 3 = state groups across waves

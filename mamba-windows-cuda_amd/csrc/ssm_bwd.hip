@@ -16,17 +16,26 @@
 // in reverse in chunks of 16 steps; each chunk restarts from the fp32
 // checkpoint the forward stored, recomputes the chunk's states and decay
 // factors into VGPRs (one exp per state) and runs the reverse sweep. Inputs
-// are staged through LDS exactly as in the forward (fp32 delta, delta*u, u,
-// dout rows per channel; B/C rows per step), double-buffered with the previous
-// chunk's global loads in flight. Sums over n (du, ddelta) are DPP reductions
-// inside the lane group. Sums over channels (dB, dC) go through a wave-private
-// LDS slab: each step the lanes deposit g_t and h_t, and every 4 steps the
-// wave folds its channels with one FMA per state against the per-channel
-// weights (delta*u for dB, dout for dC) read from the staged tile; once per
-// chunk the workgroup's waves are added and written as a per-group fp32
-// partial, which a second small kernel sums in fixed order (deterministic, no
-// atomics). dA and dD accumulate in registers over t and are summed over b by
-// the finishing kernel.
+// are staged through LDS as in the forward (fp32 delta, delta*u, u, dout rows
+// per channel; B/C rows per step); the previous chunk's global loads are in
+// flight during the sweep and land in LDS between the chunk's two barriers.
+// Sums over n (du, ddelta) are DPP reductions inside the lane group. Sums over
+// channels (dB, dC) go through a wave-private LDS slab: each step the lanes
+// deposit g_t and h_t, and every 4 steps the wave folds its channels with one
+// FMA per state against the per-channel weights (delta*u for dB, dout for dC)
+// read from the staged tile; once per chunk the workgroup's waves are added and
+// written as a per-group fp32 partial, which a second small kernel sums in
+// fixed order (deterministic, no atomics). dA and dD accumulate in registers
+// over t and are summed over the segments and b by the finishing kernel.
+//
+// Parallelism over L: as in the forward, L is cut into segments of whole
+// chunks. The adjoint entering a segment from its right is linear in the
+// adjoint leaving the last step: g_in(s) = 2^xsum(s+1) * g_in(s+1) + G(s+1),
+// where G(j) is segment j's reverse sweep of g -> dA_t*(g + dout_t*C_t) from
+// g = 0 and xsum(j) the sum of its base-2 decay exponents. A carry kernel
+// computes (G, xsum) for every segment but the first, each cut into cfold
+// carry segments; the main kernel folds them, from dh_last, into its starting
+// adjoint.
 #include <type_traits>
 
 #include "common.h"
@@ -80,13 +89,143 @@ __device__ __forceinline__ void wave_lds_fence() {
 
 }  // namespace
 
+// Adjoint carries of the chunks after the first segment, cut into ncar carry
+// segments of cps chunks (carry segment j starts at chunk first + j*cps):
+// car_g = the reverse sweep of g -> dA_t * (g + dout_t * C_t) over the carry
+// segment from g = 0, car_x = its summed base-2 decay exponents (so it maps an
+// adjoint g arriving from its right to 2^car_x * g + car_g).
 template <typename T, int SPL>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) ssm_bwd_kernel(
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fwd_min_waves(SPL), 8)))
+ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const T* __restrict__ Cm,
+                     const T* __restrict__ dout, float* __restrict__ car_g, float* __restrict__ car_x, int Bsz,
+                     int L, int D, int nck, int nblk_d, int ncar, int first, int cps) {
+    constexpr int LPC = kNState / SPL;
+    constexpr int CPW = 64 / LPC;
+    constexpr int CPB = CPW * 4;
+    constexpr int TC = kCkptSteps;
+    constexpr int RS = TC + 4;
+    constexpr int NSG = 256 / CPB;
+    constexpr int SPG = TC / NSG;
+    static_assert(NSG * SPG == TC, "tiling");
+
+    __shared__ float s_in[2][2][CPB][RS];  // [buf][delta, dout][channel][step]
+    __shared__ float s_c[2][TC][kNState];
+
+    const int tid = threadIdx.x;
+    const int lid = xcd_remap(blockIdx.x, gridDim.x);
+    const int per_seg = nblk_d * Bsz;
+    const int seg = lid / per_seg;
+    const int b = (lid % per_seg) / nblk_d;
+    const int d0 = (lid % nblk_d) * CPB;
+    const int k0 = first + seg * cps;
+    const int k1 = min(nck, k0 + cps);
+
+    const int wave = tid >> 6, lane = tid & 63;
+    const int c = wave * CPW + lane / LPC;
+    const int n0 = (lane % LPC) * SPL;
+    const bool valid = d0 + c < D;
+    const int d = valid ? d0 + c : D - 1;
+    const int lc = tid % CPB, sg = tid / CPB;
+    const bool lvalid = d0 + lc < D;
+    const int ld_d = lvalid ? d0 + lc : D - 1;
+    const int bc_t = tid >> 4, bc_n = tid & 15;
+    const int64_t row0 = (int64_t)b * L;
+
+    float A2[SPL], gc[SPL], xs[SPL];
+    float amax2 = 0.f;
+#pragma unroll
+    for (int j = 0; j < SPL; ++j) {
+        A2[j] = ld(A + (int64_t)d * kNState + n0 + j) * kLog2e;
+        amax2 = __builtin_fmaxf(amax2, __builtin_fabsf(A2[j]));
+        gc[j] = 0.f;
+        xs[j] = 0.f;
+    }
+
+    T pd[SPG], py[SPG], pc;
+    auto issue = [&](int k) {
+#pragma unroll
+        for (int s = 0; s < SPG; ++s) {
+            const int t = min(k * TC + sg * SPG + s, L - 1);
+            const int64_t off = (row0 + t) * D + ld_d;
+            pd[s] = delta[off];
+            py[s] = dout[off];
+        }
+        pc = Cm[(row0 + min(k * TC + bc_t, L - 1)) * kNState + bc_n];
+    };
+    auto commit = [&](int k, int buf) {
+        float vd[SPG], vy[SPG];
+#pragma unroll
+        for (int s = 0; s < SPG; ++s) {
+            const bool ok = lvalid && (k * TC + sg * SPG + s < L);
+            vd[s] = ok ? static_cast<float>(pd[s]) : 0.f;
+            vy[s] = ok ? static_cast<float>(py[s]) : 0.f;
+        }
+        stv<SPG>(&s_in[buf][0][lc][sg * SPG], vd);
+        stv<SPG>(&s_in[buf][1][lc][sg * SPG], vy);
+        s_c[buf][bc_t][bc_n] = static_cast<float>(pc);
+    };
+
+    if (k0 < k1) {
+        issue(k1 - 1);
+        commit(k1 - 1, (k1 - 1) & 1);
+    }
+    __syncthreads();
+    for (int k = k1 - 1; k >= k0; --k) {
+        const int buf = k & 1;
+        const bool more = k > k0;
+        if (more) issue(k - 1);
+        float dt[TC], yo[TC], Cv[TC][SPL];
+        ldv<TC>(&s_in[buf][0][c][0], dt);
+        ldv<TC>(&s_in[buf][1][c][0], yo);
+#pragma unroll
+        for (int i = 0; i < TC; ++i) ldv<SPL>(&s_c[buf][i][n0], Cv[i]);
+        float dmax = 0.f;
+#pragma unroll
+        for (int i = 0; i < TC; ++i) dmax = __builtin_fmaxf(dmax, __builtin_fabsf(dt[i]));
+        const bool need_clamp = __builtin_amdgcn_ballot_w64(dmax * amax2 > kExp2Clamp) != 0;
+        auto run = [&](auto clamp_tag) {
+            constexpr bool CLAMP = decltype(clamp_tag)::value;
+#pragma unroll
+            for (int i = TC - 1; i >= 0; --i) {
+#pragma unroll
+                for (int j = 0; j < SPL; ++j) {
+                    float x = dt[i] * A2[j];
+                    if constexpr (CLAMP) {
+                        x = __builtin_fminf(__builtin_fmaxf(x, -kExp2Clamp), kExp2Clamp);
+                        xs[j] += x;
+                    }
+                    gc[j] = __builtin_amdgcn_exp2f(x) * __builtin_fmaf(yo[i], Cv[i][j], gc[j]);
+                }
+            }
+        };
+        if (need_clamp) {
+            run(std::true_type{});
+        } else {
+            run(std::false_type{});
+            float sdt = 0.f;
+#pragma unroll
+            for (int i = 0; i < TC; ++i) sdt += dt[i];
+#pragma unroll
+            for (int j = 0; j < SPL; ++j) xs[j] = __builtin_fmaf(A2[j], sdt, xs[j]);
+        }
+        if (more) commit(k - 1, buf ^ 1);
+        __syncthreads();
+    }
+    if (valid) {
+        const int64_t o = (((int64_t)b * ncar + seg) * D + d) * kNState + n0;
+        stv<SPL>(car_g + o, gc);
+        stv<SPL>(car_x + o, xs);
+    }
+}
+
+template <typename T, int SPL>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_min_waves(SPL), 8))) ssm_bwd_kernel(
     const T* __restrict__ u, const T* __restrict__ delta, const T* __restrict__ A, const T* __restrict__ Bm,
     const T* __restrict__ Cm, const T* __restrict__ Dv, const T* __restrict__ dout, const T* __restrict__ dh_last,
     const float* __restrict__ ckpt, T* __restrict__ du, T* __restrict__ ddelta, T* __restrict__ dh_prev,
-    float* __restrict__ dA_part, float* __restrict__ dD_part, float* __restrict__ dbc_part, int Bsz, int L, int D,
-    int nck, int nblk_d) {
+    float* __restrict__ dA_part, float* __restrict__ dD_part, float* __restrict__ dbc_part,
+    const float* __restrict__ car_g, const float* __restrict__ car_x, int Bsz, int L, int D, int nck, int nblk_d,
+    int nseg, int cps, int ncar, int cfold) {
     constexpr int LPC = kNState / SPL;
     constexpr int CPW = 64 / LPC;
     constexpr int CPB = CPW * 4;
@@ -98,25 +237,28 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
     constexpr int HALF = CPW / 2;  // channels each folding lane sums
     static_assert(NSG * SPG == TC && CPW >= 2, "tiling");
 
-    // [buf][delta, delta*u, u, dout] planes of [channel][step]; planes are AS floats apart
+    // [delta, delta*u, u, dout] planes of [channel][step]; planes are AS floats apart
     // (AS = 16 mod 64 banks) so the delta*u and dout weights of one channel sit in different banks
     constexpr int AS = CPB * RS + 16;
-    __shared__ float s_in_raw[2][4 * AS];
-    __shared__ float s_bc[2][TC][2 * kNState];
-    // wave-private slabs of g_t (plane 0) and h_t (plane 1): [wave][plane][half][slot][channel][16];
+    __shared__ float s_in_raw[4 * AS];
+    __shared__ float s_bc[TC][2 * kNState];
+    // wave-private slabs of g_t (plane 0) and h_t (plane 1): [wave][plane][slot][channel][16];
     // a 16-lane group deposits 64 consecutive floats, plane 1 is offset by 32 banks
-    constexpr int SLAB = 2 * kRedSlots * CPW * kNState + 32;
-    __shared__ float s_red[4][2 * SLAB];
-    auto s_in = [&](int buf, int plane, int ch) -> float* { return &s_in_raw[buf][plane * AS + ch * RS]; };
-    // single-buffered: a second barrier after the store phase protects them
+    constexpr int PL = kRedSlots * CPW * kNState + 32;
+    __shared__ float s_red[4][2 * PL];
+    auto s_in = [&](int plane, int ch) -> float* { return &s_in_raw[plane * AS + ch * RS]; };
     __shared__ float s_part[4][TC][2 * kNState];
     __shared__ float s_out[2][TC][OS];  // [du, ddelta][step][channel]
 
     const int tid = threadIdx.x;
     const int lid = xcd_remap(blockIdx.x, gridDim.x);
-    const int b = lid / nblk_d;
+    const int per_seg = nblk_d * Bsz;
+    const int seg = lid / per_seg;
+    const int b = (lid % per_seg) / nblk_d;
     const int blk = lid % nblk_d;
     const int d0 = blk * CPB;
+    const int k0 = seg * cps;
+    const int k1 = min(nck, k0 + cps);
 
     const int wave = tid >> 6, lane = tid & 63;
     const int cw = lane / LPC;  // channel within the wave
@@ -140,8 +282,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
     for (int j = 0; j < SPL; ++j) {
         An[j] = ld(A + (int64_t)d * kNState + n0 + j);
         A2[j] = An[j] * kLog2e;
-        gc[j] = (dh_last != nullptr && valid) ? ld(dh_last + ((int64_t)b * D + d) * kNState + n0 + j) : 0.f;
+        gc[j] = dh_last != nullptr ? ld(dh_last + ((int64_t)b * D + d) * kNState + n0 + j) : 0.f;
         dAacc[j] = 0.f;
+    }
+    for (int j = ncar - 1; j >= seg * cfold; --j) {  // g -> 2^xsum * g + G of each following carry segment
+        const int64_t o = (((int64_t)b * ncar + j) * D + d) * kNState + n0;
+        float cg[SPL], cx[SPL];
+        ldv<SPL>(car_g + o, cg);
+        ldv<SPL>(car_x + o, cx);
+#pragma unroll
+        for (int q = 0; q < SPL; ++q) gc[q] = __builtin_fmaf(__builtin_amdgcn_exp2f(cx[q]), gc[q], cg[q]);
     }
     float dDacc = 0.f;
     const float Dd = ld(Dv + d);
@@ -163,7 +313,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
         pc = Cm[(row0 + t) * kNState + bc_n];
         ldv<SPL>(ckb + (int64_t)k * D * kNState, hnext);
     };
-    auto commit = [&](int k, int buf) {
+    auto commit = [&](int k) {
         float vd[SPG], vdu[SPG], vu[SPG], vy[SPG];
 #pragma unroll
         for (int s = 0; s < SPG; ++s) {
@@ -173,40 +323,40 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
             vy[s] = ok ? static_cast<float>(py[s]) : 0.f;
             vdu[s] = vd[s] * vu[s];
         }
-        stv<SPG>((s_in(buf, 0, lc) + sg * SPG), vd);
-        stv<SPG>((s_in(buf, 1, lc) + sg * SPG), vdu);
-        stv<SPG>((s_in(buf, 2, lc) + sg * SPG), vu);
-        stv<SPG>((s_in(buf, 3, lc) + sg * SPG), vy);
-        s_bc[buf][bc_t][bc_n] = static_cast<float>(pb);
-        s_bc[buf][bc_t][kNState + bc_n] = static_cast<float>(pc);
+        stv<SPG>((s_in(0, lc) + sg * SPG), vd);
+        stv<SPG>((s_in(1, lc) + sg * SPG), vdu);
+        stv<SPG>((s_in(2, lc) + sg * SPG), vu);
+        stv<SPG>((s_in(3, lc) + sg * SPG), vy);
+        s_bc[bc_t][bc_n] = static_cast<float>(pb);
+        s_bc[bc_t][kNState + bc_n] = static_cast<float>(pc);
     };
 
     float hin[SPL];
-    if (nck > 0) {  // L == 0 has no chunk; the outputs below are then dh_prev = dh_last and zero partials
-        issue(nck - 1);
-        commit(nck - 1, (nck - 1) & 1);
+    if (k0 < k1) {  // L == 0 has no chunk; the outputs below are then dh_prev = dh_last and zero partials
+        issue(k1 - 1);
+        commit(k1 - 1);
 #pragma unroll
         for (int j = 0; j < SPL; ++j) hin[j] = hnext[j];
     }
     __syncthreads();
 
-    float* red_g = &s_red[wave][0];     // [half][slot][channel][16]
-    float* red_h = &s_red[wave][SLAB];  // [half][slot][channel][16]
+    float* red_g = &s_red[wave][0];   // [slot][channel][16]
+    float* red_h = &s_red[wave][PL];  // [slot][channel][16]
     float amax2 = 0.f;
 #pragma unroll
     for (int j = 0; j < SPL; ++j) amax2 = __builtin_fmaxf(amax2, __builtin_fabsf(A2[j]));
 
-    for (int k = nck - 1; k >= 0; --k) {
-        const int buf = k & 1;
+    for (int k = k1 - 1; k >= k0; --k) {
         const int t0 = k * TC;
-        if (k > 0) issue(k - 1);
+        const bool more = k > k0;
+        if (more) issue(k - 1);
 
         // ---- recompute the chunk's states (one exp per state) ----
         float H[TC][SPL], E[TC][SPL], dt[TC];
         {
             float dtu[TC];
-            ldv<TC>(s_in(buf, 0, c), dt);
-            ldv<TC>(s_in(buf, 1, c), dtu);
+            ldv<TC>(s_in(0, c), dt);
+            ldv<TC>(s_in(1, c), dtu);
             float dmax = 0.f;
 #pragma unroll
             for (int i = 0; i < TC; ++i) dmax = __builtin_fmaxf(dmax, __builtin_fabsf(dt[i]));
@@ -219,7 +369,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
 #pragma unroll
                 for (int i = 0; i < TC; ++i) {
                     float Bv[SPL];
-                    ldv<SPL>(&s_bc[buf][i][n0], Bv);
+                    ldv<SPL>(&s_bc[i][n0], Bv);
 #pragma unroll
                     for (int j = 0; j < SPL; ++j) {
                         const float x = dt[i] * A2[j];
@@ -235,15 +385,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
                 recompute(std::false_type{});
         }
         // ---- reverse sweep ----
-        // LDS operands are read one step (B, C) or one 4-step group (u, dout) ahead of use,
-        // and the channel fold of a 4-step phase runs one phase later from the other half
-        // of the double-buffered slab, so no LDS read waits on a just-issued access.
+        // B/C are read one step ahead and u/dout one 4-step group ahead of use; every 4 steps the
+        // wave folds the phase's deposits over its channels.
         auto fold = [&](int phase) {
-            const float* base_g = red_g + (phase & 1) * (kRedSlots * CPW * kNState);
-            const float* base_h = red_h + (phase & 1) * (kRedSlots * CPW * kNState);
             const bool is_c = rq >= 4;
-            const float* plane = is_c ? base_h : base_g;
-            const float* wrow = s_in(buf, is_c ? 3 : 1, wave * CPW) + phase * kRedSlots + rs;
+            const float* plane = is_c ? red_h : red_g;
+            const float* wrow = s_in(is_c ? 3 : 1, wave * CPW) + phase * kRedSlots + rs;
             const int q4 = (rq & 3) * 4;
             float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -260,10 +407,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
             if (rhalf == 0) stv<4>(&s_part[wave][phase * kRedSlots + rs][rq * 4], acc);
         };
         float uq[4], yq[4], uqn[4], yqn[4], Bn[SPL], Cn[SPL];
-        ldv<4>(s_in(buf, 2, c) + TC - 4, uqn);
-        ldv<4>(s_in(buf, 3, c) + TC - 4, yqn);
-        ldv<SPL>(&s_bc[buf][TC - 1][n0], Bn);
-        ldv<SPL>(&s_bc[buf][TC - 1][kNState + n0], Cn);
+        ldv<4>(s_in(2, c) + TC - 4, uqn);
+        ldv<4>(s_in(3, c) + TC - 4, yqn);
+        ldv<SPL>(&s_bc[TC - 1][n0], Bn);
+        ldv<SPL>(&s_bc[TC - 1][kNState + n0], Cn);
 #pragma unroll
         for (int i = TC - 1; i >= 0; --i) {
             const int slot = i % kRedSlots, phase = i / kRedSlots;
@@ -274,8 +421,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
                     yq[q] = yqn[q];
                 }
                 if (i >= 4) {
-                    ldv<4>(s_in(buf, 2, c) + i - 7, uqn);
-                    ldv<4>(s_in(buf, 3, c) + i - 7, yqn);
+                    ldv<4>(s_in(2, c) + i - 7, uqn);
+                    ldv<4>(s_in(3, c) + i - 7, yqn);
                 }
             }
             float Bv[SPL], Cv[SPL];
@@ -285,8 +432,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
                 Cv[j] = Cn[j];
             }
             if (i > 0) {
-                ldv<SPL>(&s_bc[buf][i > 0 ? i - 1 : 0][n0], Bn);
-                ldv<SPL>(&s_bc[buf][i > 0 ? i - 1 : 0][kNState + n0], Cn);
+                ldv<SPL>(&s_bc[i > 0 ? i - 1 : 0][n0], Bn);
+                ldv<SPL>(&s_bc[i > 0 ? i - 1 : 0][kNState + n0], Cn);
             }
             const float ui = uq[slot], yo = yq[slot];
             float gt[SPL];
@@ -307,32 +454,30 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
             s_out[0][i][c] = __builtin_fmaf(Dd, yo, dt[i] * r1);
             s_out[1][i][c] = __builtin_fmaf(ui, r1, r2);
             dDacc = __builtin_fmaf(yo, ui, dDacc);
-            const int sl = ((phase & 1) * kRedSlots + slot) * CPW + cw;
+            const int sl = slot * CPW + cw;
             stv<SPL>(red_g + sl * kNState + n0, gt);
             stv<SPL>(red_h + sl * kNState + n0, H[i]);
-            if (slot == 0 && phase + 1 < TC / kRedSlots) {
+            if (slot == 0) {
                 wave_lds_fence();
-                fold(phase + 1);
+                fold(phase);
+                wave_lds_fence();
             }
         }
-        wave_lds_fence();
-        fold(0);
-        wave_lds_fence();
-        if (k > 0) {
-            commit(k - 1, buf ^ 1);
+        __syncthreads();  // every wave is done with the staged chunk and has written s_out / s_part
+        if (more) {
+            commit(k - 1);
 #pragma unroll
             for (int j = 0; j < SPL; ++j) hin[j] = hnext[j];
         }
-        __syncthreads();
         // coalesced du / ddelta tile stores: thread -> (step, VPT channels)
         {
             constexpr int VPT = CPB / 16;
-            const int st_ = tid >> 4, cq = (tid & 15) * VPT;
-            const int t = t0 + st_;
+            const int sr = tid >> 4, cq = (tid & 15) * VPT;
+            const int t = t0 + sr;
             if (t < L) {
                 float a[VPT], bb[VPT];
-                ldv<VPT>(&s_out[0][st_][cq], a);
-                ldv<VPT>(&s_out[1][st_][cq], bb);
+                ldv<VPT>(&s_out[0][sr][cq], a);
+                ldv<VPT>(&s_out[1][sr][cq], bb);
                 T* pdu = du + (row0 + t) * D + d0 + cq;
                 T* pdd = ddelta + (row0 + t) * D + d0 + cq;
 #pragma unroll
@@ -349,16 +494,17 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
             const float s = s_part[0][tt][v] + s_part[1][tt][v] + s_part[2][tt][v] + s_part[3][tt][v];
             if (t0 + tt < L) dbc_part[(((int64_t)blk * Bsz + b) * L + t0 + tt) * 32 + v] = s;
         }
-        __syncthreads();  // s_out / s_part are rewritten by the next chunk
+        __syncthreads();  // the next chunk's tile is staged; s_out / s_part are free again
     }
 
     if (valid) {
-        if (dh_prev != nullptr) {
+        if (dh_prev != nullptr && seg == 0) {
 #pragma unroll
             for (int j = 0; j < SPL; ++j) st(dh_prev + ((int64_t)b * D + d) * kNState + n0 + j, gc[j]);
         }
-        stv<SPL>(dA_part + ((int64_t)b * D + d) * kNState + n0, dAacc);
-        if (g == 0) dD_part[(int64_t)b * D + d] = dDacc;
+        const int64_t pr = (int64_t)seg * Bsz + b;  // partial row
+        stv<SPL>(dA_part + (pr * D + d) * kNState + n0, dAacc);
+        if (g == 0) dD_part[pr * D + d] = dDacc;
     }
 }
 
@@ -378,21 +524,21 @@ __global__ void __launch_bounds__(256) bwd_finish_bc_kernel(const float* __restr
         st(dC + r * kNState + v - kNState, s);
 }
 
-// dA (D,N) and dD (D,): sum the per-batch partials in batch order and cast.
+// dA (D,N) and dD (D,): sum the nrows (segment, batch) partials in order and cast.
 template <typename T>
 __global__ void __launch_bounds__(256) bwd_finish_ad_kernel(const float* __restrict__ dA_part,
                                                             const float* __restrict__ dD_part, T* __restrict__ dA,
-                                                            T* __restrict__ dD, int Bsz, int D) {
+                                                            T* __restrict__ dD, int nrows, int D) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t nA = (int64_t)D * kNState;
     if (i < nA) {
         float s = 0.f;
-        for (int b = 0; b < Bsz; ++b) s += dA_part[(int64_t)b * nA + i];
+        for (int r = 0; r < nrows; ++r) s += dA_part[(int64_t)r * nA + i];
         st(dA + i, s);
     } else if (i < nA + D) {
         const int64_t dd = i - nA;
         float s = 0.f;
-        for (int b = 0; b < Bsz; ++b) s += dD_part[(int64_t)b * D + dd];
+        for (int r = 0; r < nrows; ++r) s += dD_part[(int64_t)r * D + dd];
         st(dD + dd, s);
     }
 }
@@ -403,30 +549,25 @@ int bwd_groups(const SsmShape& s, int spl) {
 }
 
 template <typename T, int SPL>
-static hipError_t bwd_inst(const void* u, const void* delta, const void* A, const void* B, const void* C,
-                           const void* Dv, const void* dout, const void* dh_last, const float* ckpt, void* du,
-                           void* ddelta, void* dh_prev, float* dA_part, float* dD_part, float* dbc_part,
-                           const SsmShape& s, hipStream_t st) {
+static hipError_t bwd_inst(const BwdArgs& a, const SsmShape& s, hipStream_t st) {
     const int nblk_d = bwd_groups(s, SPL);
     const int nck = (int)((s.seqlen + kCkptSteps - 1) / kCkptSteps);
-    const int grid = nblk_d * (int)s.batch;
-    hipLaunchKernelGGL((ssm_bwd_kernel<T, SPL>), dim3(grid), dim3(256), 0, st, (const T*)u, (const T*)delta,
-                       (const T*)A, (const T*)B, (const T*)C, (const T*)Dv, (const T*)dout, (const T*)dh_last, ckpt,
-                       (T*)du, (T*)ddelta, (T*)dh_prev, dA_part, dD_part, dbc_part, (int)s.batch, (int)s.seqlen,
-                       (int)s.dim, nck, nblk_d);
+    const int per_seg = nblk_d * (int)s.batch;
+    if (a.nseg > 1)  // carries of every chunk after the first segment
+        hipLaunchKernelGGL((ssm_bwd_carry_kernel<T, SPL>), dim3(per_seg * a.ncar), dim3(256), 0, st,
+                           (const T*)a.delta, (const T*)a.A, (const T*)a.C, (const T*)a.dout, a.car_g, a.car_x,
+                           (int)s.batch, (int)s.seqlen, (int)s.dim, nck, nblk_d, a.ncar, a.cps, a.cps / a.cfold);
+    hipLaunchKernelGGL((ssm_bwd_kernel<T, SPL>), dim3(per_seg * a.nseg), dim3(256), 0, st, (const T*)a.u,
+                       (const T*)a.delta, (const T*)a.A, (const T*)a.B, (const T*)a.C, (const T*)a.Dv,
+                       (const T*)a.dout, (const T*)a.dh_last, a.ckpt, (T*)a.du, (T*)a.ddelta, (T*)a.dh_prev,
+                       a.dA_part, a.dD_part, a.dbc_part, a.car_g, a.car_x, (int)s.batch, (int)s.seqlen, (int)s.dim,
+                       nck, nblk_d, a.nseg, a.cps, a.ncar, a.cfold);
     return hipGetLastError();
 }
 
-hipError_t launch_ssm_bwd(bool is_half, int spl, const void* u, const void* delta, const void* A, const void* B,
-                          const void* C, const void* Dv, const void* dout, const void* dh_last, const float* ckpt,
-                          void* du, void* ddelta, void* dh_prev, float* dA_part, float* dD_part, float* dbc_part,
-                          const SsmShape& s, hipStream_t st) {
-#define MWC_BWD_SPL(S)                                                                                           \
-    if (spl == S)                                                                                                \
-        return is_half ? bwd_inst<half_t, S>(u, delta, A, B, C, Dv, dout, dh_last, ckpt, du, ddelta, dh_prev,   \
-                                             dA_part, dD_part, dbc_part, s, st)                                  \
-                       : bwd_inst<float, S>(u, delta, A, B, C, Dv, dout, dh_last, ckpt, du, ddelta, dh_prev,    \
-                                            dA_part, dD_part, dbc_part, s, st);
+hipError_t launch_ssm_bwd(bool is_half, int spl, const BwdArgs& a, const SsmShape& s, hipStream_t st) {
+#define MWC_BWD_SPL(S) \
+    if (spl == S) return is_half ? bwd_inst<half_t, S>(a, s, st) : bwd_inst<float, S>(a, s, st);
     MWC_BWD_SPL(1)
     MWC_BWD_SPL(2)
     MWC_BWD_SPL(4)
@@ -436,23 +577,23 @@ hipError_t launch_ssm_bwd(bool is_half, int spl, const void* u, const void* delt
 
 template <typename T>
 static hipError_t finish_t(const float* dbc_part, const float* dA_part, const float* dD_part, void* dB, void* dC,
-                           void* dA, void* dD, int ngrp, const SsmShape& s, hipStream_t st) {
+                           void* dA, void* dD, int ngrp, int nrows, const SsmShape& s, hipStream_t st) {
     const int64_t rows = s.batch * s.seqlen;
     const int g1 = (int)((rows * 32 + 255) / 256);
     if (g1 > 0)
         hipLaunchKernelGGL(bwd_finish_bc_kernel<T>, dim3(g1), dim3(256), 0, st, dbc_part, (T*)dB, (T*)dC, ngrp, rows);
     const int64_t n2 = s.dim * kNState + s.dim;
     const int g2 = (int)((n2 + 255) / 256);
-    hipLaunchKernelGGL(bwd_finish_ad_kernel<T>, dim3(g2), dim3(256), 0, st, dA_part, dD_part, (T*)dA, (T*)dD,
-                       (int)s.batch, (int)s.dim);
+    hipLaunchKernelGGL(bwd_finish_ad_kernel<T>, dim3(g2), dim3(256), 0, st, dA_part, dD_part, (T*)dA, (T*)dD, nrows,
+                       (int)s.dim);
     return hipGetLastError();
 }
 
 hipError_t launch_bwd_finish(bool is_half, const float* dbc_part, const float* dA_part, const float* dD_part,
-                             void* dB, void* dC, void* dA, void* dD, int ngroups, const SsmShape& s,
+                             void* dB, void* dC, void* dA, void* dD, int ngroups, int nrows, const SsmShape& s,
                              hipStream_t st) {
-    return is_half ? finish_t<half_t>(dbc_part, dA_part, dD_part, dB, dC, dA, dD, ngroups, s, st)
-                   : finish_t<float>(dbc_part, dA_part, dD_part, dB, dC, dA, dD, ngroups, s, st);
+    return is_half ? finish_t<half_t>(dbc_part, dA_part, dD_part, dB, dC, dA, dD, ngroups, nrows, s, st)
+                   : finish_t<float>(dbc_part, dA_part, dD_part, dB, dC, dA, dD, ngroups, nrows, s, st);
 }
 
 }  // namespace mwc

@@ -7,9 +7,18 @@
 // Mapping (not the reference's one-warp-per-channel serial loop): a channel's
 // 16 states are spread over a group of LPC = 16/SPL consecutive lanes, each
 // lane holding SPL states in VGPRs; a 64-lane wave scans 64/LPC channels and a
-// 4-wave workgroup CPB = 4*64/LPC channels of one batch row, walking L in
-// chunks of 16 steps. The C-contraction is an in-register FMA chain plus a DPP
-// all-reduce inside the lane group.
+// 4-wave workgroup CPB = 4*64/LPC channels of one batch row, walking its part
+// of L in chunks of 16 steps. The C-contraction is an in-register FMA chain
+// plus a DPP all-reduce inside the lane group.
+//
+// Parallelism over L: the sequence is cut into `nseg` segments of whole chunks
+// so that the grid fills every SIMD evenly. A carry pass (FwdMode kCarry) cuts
+// every segment but the last into `cfold` carry segments, runs each from h = 0
+// and records its end state and, per state, the sum of its base-2 decay
+// exponents, so that it acts on an incoming state as h -> 2^xsum * h + h_end.
+// The main pass (kMain, or kState when only checkpoints are wanted) folds the
+// preceding carries into its starting state, in sequence order, and runs its
+// segment.
 //
 // Data movement: the workgroup stages each chunk's inputs through LDS --
 // delta, delta*u and u as fp32 rows per channel (converted once, read back by
@@ -18,9 +27,8 @@
 // computed, so one barrier per chunk is the only synchronisation. Outputs go
 // through an LDS tile and leave as coalesced row stores. Steps past L are
 // padded with delta = u = 0, which leaves the state unchanged, so the inner
-// loop carries no bounds checks. With at most one wave per SIMD at the target
-// shapes every issued instruction costs the wave 4 cycles, so the design
-// minimises instructions per state, not just VALU work.
+// loop carries no bounds checks. The [-88, 88] clamp of the exponent runs only
+// in chunks where |delta|*max|A| can reach it (a wave-uniform test).
 #include <type_traits>
 
 #include "common.h"
@@ -61,13 +69,18 @@ __device__ __forceinline__ void vst(float* p, const float (&v)[K]) {
     }
 }
 
-template <typename T, int SPL, bool HAS_OUT>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta,
-                                                      const T* __restrict__ A, const T* __restrict__ Bm,
-                                                      const T* __restrict__ Cm, const T* __restrict__ Dv,
-                                                      const T* __restrict__ h_prev, T* __restrict__ out,
-                                                      T* __restrict__ h_last, float* __restrict__ ckpt, int L, int D,
-                                                      int nck, int nblk_d) {
+
+enum FwdMode { kMain = 0, kState = 1, kCarry = 2 };
+
+template <typename T, int SPL, int MODE>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fwd_min_waves(SPL), 8)))
+ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __restrict__ A,
+               const T* __restrict__ Bm, const T* __restrict__ Cm, const T* __restrict__ Dv,
+               const T* __restrict__ h_prev, T* __restrict__ out, T* __restrict__ h_last, float* __restrict__ ckpt,
+               float* __restrict__ car_h, float* __restrict__ car_x, int Bsz, int L, int D, int nck, int nblk_d,
+               int nseg, int cps, int ncar, int cfold) {
+    constexpr bool HAS_OUT = MODE == kMain;
+    constexpr bool CARRY = MODE == kCarry;
     constexpr int LPC = kNState / SPL;  // lanes per channel
     constexpr int CPW = 64 / LPC;       // channels per wave
     constexpr int CPB = CPW * 4;        // channels per workgroup
@@ -76,16 +89,21 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
     constexpr int NSG = 256 / CPB;      // loader step groups
     constexpr int SPG = TC / NSG;       // steps per loader thread
     constexpr int YS = CPB + 4;         // LDS row stride of the output tile
+    constexpr int NPL = HAS_OUT ? 3 : 2;
     static_assert(NSG * SPG == TC, "loader tiling");
 
-    __shared__ float s_in[2][3][CPB][RS];  // [buf][delta, delta*u, u][channel][step]
-    __shared__ float s_bc[2][TC][2 * kNState];
+    __shared__ float s_in[2][NPL][CPB][RS];  // [buf][delta, delta*u, u][channel][step]
+    __shared__ float s_bc[2][TC][HAS_OUT ? 2 * kNState : kNState];
     __shared__ float s_y[HAS_OUT ? 2 : 1][HAS_OUT ? TC : 1][HAS_OUT ? YS : 1];
 
     const int tid = threadIdx.x;
     const int lid = xcd_remap(blockIdx.x, gridDim.x);
-    const int b = lid / nblk_d;
+    const int per_seg = nblk_d * Bsz;
+    const int seg = lid / per_seg;
+    const int b = (lid % per_seg) / nblk_d;
     const int d0 = (lid % nblk_d) * CPB;
+    const int k0 = seg * cps;
+    const int k1 = min(nck, k0 + cps);
 
     // consumer role
     const int wave = tid >> 6, lane = tid & 63;
@@ -101,17 +119,29 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
     const int ld_d = lvalid ? d0 + lc : D - 1;
     const int bc_t = tid >> 4, bc_n = tid & 15;
     const int64_t row0 = (int64_t)b * L;
+    // carries of the ncar carry segments (cfold per main segment): car_[b][carry segment][d][n]
+    const int64_t car0 = ((int64_t)b * ncar * D + d) * kNState + n0;
+    const int64_t car_seg = (int64_t)D * kNState;
 
-    float A2[SPL], h[SPL];
+    float A2[SPL], h[SPL], xs[SPL];
+    float amax2 = 0.f;  // max_j |A_j| * log2(e) over this lane's states
 #pragma unroll
     for (int j = 0; j < SPL; ++j) {
         A2[j] = ld(A + (int64_t)d * kNState + n0 + j) * kLog2e;
-        h[j] = h_prev ? ld(h_prev + ((int64_t)b * D + d) * kNState + n0 + j) : 0.f;
+        amax2 = __builtin_fmaxf(amax2, __builtin_fabsf(A2[j]));
+        h[j] = (!CARRY && h_prev) ? ld(h_prev + ((int64_t)b * D + d) * kNState + n0 + j) : 0.f;
+        xs[j] = 0.f;
+    }
+    if constexpr (!CARRY) {
+        for (int j = 0; j < seg * cfold; ++j) {  // h -> 2^xsum * h + h_end of each preceding carry segment
+            float ch[SPL], cx[SPL];
+            lds_ld<SPL>(car_h + car0 + j * car_seg, ch);
+            lds_ld<SPL>(car_x + car0 + j * car_seg, cx);
+#pragma unroll
+            for (int q = 0; q < SPL; ++q) h[q] = __builtin_fmaf(__builtin_amdgcn_exp2f(cx[q]), h[q], ch[q]);
+        }
     }
     const float Dd = ld(Dv + d);
-    float amax2 = 0.f;  // max_j |A_j| * log2(e) over this lane's states
-#pragma unroll
-    for (int j = 0; j < SPL; ++j) amax2 = __builtin_fmaxf(amax2, __builtin_fabsf(A2[j]));
 
     T pu[SPG], pd[SPG], pb, pc;
     auto issue = [&](int k) {
@@ -137,21 +167,21 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
         }
         vst<SPG>(&s_in[buf][0][lc][sg * SPG], vd);
         vst<SPG>(&s_in[buf][1][lc][sg * SPG], vdu);
-        vst<SPG>(&s_in[buf][2][lc][sg * SPG], vu);
+        if constexpr (HAS_OUT) vst<SPG>(&s_in[buf][2][lc][sg * SPG], vu);
         s_bc[buf][bc_t][bc_n] = static_cast<float>(pb);
         if constexpr (HAS_OUT) s_bc[buf][bc_t][kNState + bc_n] = static_cast<float>(pc);
     };
 
-    if (nck > 0) {  // L == 0: no chunk, h_last = h_prev
-        issue(0);
-        commit(0, 0);
+    if (k0 < k1) {  // every segment holds a chunk unless L == 0 (then h_last = h_prev)
+        issue(k0);
+        commit(k0, k0 & 1);
     }
     __syncthreads();
-    float* ckb = ckpt ? ckpt + ((int64_t)b * nck * D + d) * kNState + n0 : nullptr;
+    float* ckb = (!CARRY && ckpt) ? ckpt + ((int64_t)b * nck * D + d) * kNState + n0 : nullptr;
 
-    for (int k = 0; k < nck; ++k) {
+    for (int k = k0; k < k1; ++k) {
         const int buf = k & 1;
-        const bool more = k + 1 < nck;
+        const bool more = k + 1 < k1;
         if (more) issue(k + 1);
         if (ckb != nullptr && valid) vst<SPL>(ckb + (int64_t)k * D * kNState, h);
 
@@ -177,9 +207,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
                 float y = 0.f;
 #pragma unroll
                 for (int j = 0; j < SPL; ++j) {
-                    const float x = dt[i] * A2[j];
-                    const float e = CLAMP ? exp2_clamped(x) : __builtin_amdgcn_exp2f(x);
-                    h[j] = __builtin_fmaf(e, h[j], dtu[i] * Bv[i][j]);
+                    float x = dt[i] * A2[j];
+                    if constexpr (CLAMP) {
+                        x = __builtin_fminf(__builtin_fmaxf(x, -kExp2Clamp), kExp2Clamp);
+                        if constexpr (CARRY) xs[j] += x;
+                    }
+                    h[j] = __builtin_fmaf(__builtin_amdgcn_exp2f(x), h[j], dtu[i] * Bv[i][j]);
                     if constexpr (HAS_OUT) y = __builtin_fmaf(Cv[i][j], h[j], y);
                 }
                 if constexpr (HAS_OUT) {
@@ -189,20 +222,28 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
                 }
             }
         };
-        if (need_clamp)
+        if (need_clamp) {
             run(std::true_type{});
-        else
+        } else {
             run(std::false_type{});
+            if constexpr (CARRY) {
+                float sdt = 0.f;
+#pragma unroll
+                for (int i = 0; i < TC; ++i) sdt += dt[i];
+#pragma unroll
+                for (int j = 0; j < SPL; ++j) xs[j] = __builtin_fmaf(A2[j], sdt, xs[j]);
+            }
+        }
         if (more) commit(k + 1, buf ^ 1);
         __syncthreads();
         if constexpr (HAS_OUT) {
-            // coalesced store of the chunk's output tile: thread -> (step, SPG channels)
-            constexpr int VPT = CPB / (256 / TC);  // channels per thread
-            const int st = tid / (CPB / VPT), cq = (tid % (CPB / VPT)) * VPT;
-            const int t = k * TC + st;
+            // coalesced store of the chunk's output tile: thread -> (step, VPT channels)
+            constexpr int VPT = CPB / (256 / TC);
+            const int sr = tid / (CPB / VPT), cq = (tid % (CPB / VPT)) * VPT;
+            const int t = k * TC + sr;
             if (t < L) {
                 float v[VPT];
-                lds_ld<VPT>(&s_y[buf][st][cq], v);
+                lds_ld<VPT>(&s_y[buf][sr][cq], v);
                 T* op = out + (row0 + t) * D + d0 + cq;
 #pragma unroll
                 for (int q = 0; q < VPT; ++q)
@@ -210,38 +251,43 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
             }
         }
     }
-    if (h_last != nullptr && valid) {
+    if constexpr (CARRY) {
+        if (valid) {
+            vst<SPL>(car_h + car0 + seg * car_seg, h);
+            vst<SPL>(car_x + car0 + seg * car_seg, xs);
+        }
+    } else if (h_last != nullptr && valid && seg == nseg - 1) {
 #pragma unroll
         for (int j = 0; j < SPL; ++j) st(h_last + ((int64_t)b * D + d) * kNState + n0 + j, h[j]);
     }
 }
 
-template <typename T, int SPL>
-static hipError_t fwd_inst(const void* u, const void* delta, const void* A, const void* B, const void* C,
-                           const void* Dv, const void* h_prev, void* out, void* h_last, float* ckpt,
-                           const SsmShape& s, hipStream_t st) {
+template <typename T, int SPL, int MODE>
+static void fwd_launch(const FwdArgs& a, const SsmShape& s, int nseg_launched, hipStream_t st) {
     constexpr int CPB = 4 * 64 / (kNState / SPL);
     const int nblk_d = (int)((s.dim + CPB - 1) / CPB);
-    const int grid = nblk_d * (int)s.batch;
     const int nck = (int)((s.seqlen + kCkptSteps - 1) / kCkptSteps);
-    if (out != nullptr)
-        hipLaunchKernelGGL((ssm_fwd_kernel<T, SPL, true>), dim3(grid), dim3(256), 0, st, (const T*)u,
-                           (const T*)delta, (const T*)A, (const T*)B, (const T*)C, (const T*)Dv, (const T*)h_prev,
-                           (T*)out, (T*)h_last, ckpt, (int)s.seqlen, (int)s.dim, nck, nblk_d);
+    const int grid = nblk_d * (int)s.batch * nseg_launched;
+    hipLaunchKernelGGL((ssm_fwd_kernel<T, SPL, MODE>), dim3(grid), dim3(256), 0, st, (const T*)a.u,
+                       (const T*)a.delta, (const T*)a.A, (const T*)a.B, (const T*)a.C, (const T*)a.Dv,
+                       (const T*)a.h_prev, (T*)a.out, (T*)a.h_last, a.ckpt, a.car_h, a.car_x, (int)s.batch,
+                       (int)s.seqlen, (int)s.dim, nck, nblk_d, a.nseg, MODE == kCarry ? a.cps / a.cfold : a.cps,
+                       a.ncar, a.cfold);
+}
+
+template <typename T, int SPL>
+static hipError_t fwd_inst(const FwdArgs& a, const SsmShape& s, hipStream_t st) {
+    if (a.nseg > 1) fwd_launch<T, SPL, kCarry>(a, s, a.ncar, st);  // carries of all chunks before the last segment
+    if (a.out != nullptr)
+        fwd_launch<T, SPL, kMain>(a, s, a.nseg, st);
     else
-        hipLaunchKernelGGL((ssm_fwd_kernel<T, SPL, false>), dim3(grid), dim3(256), 0, st, (const T*)u,
-                           (const T*)delta, (const T*)A, (const T*)B, (const T*)C, (const T*)Dv, (const T*)h_prev,
-                           (T*)out, (T*)h_last, ckpt, (int)s.seqlen, (int)s.dim, nck, nblk_d);
+        fwd_launch<T, SPL, kState>(a, s, a.nseg, st);
     return hipGetLastError();
 }
 
-hipError_t launch_ssm_fwd(bool is_half, int spl, const void* u, const void* delta, const void* A, const void* B,
-                          const void* C, const void* Dv, const void* h_prev, void* out, void* h_last, float* ckpt,
-                          const SsmShape& s, hipStream_t st) {
-#define MWC_FWD_SPL(S)                                                                                     \
-    if (spl == S)                                                                                          \
-        return is_half ? fwd_inst<half_t, S>(u, delta, A, B, C, Dv, h_prev, out, h_last, ckpt, s, st)     \
-                       : fwd_inst<float, S>(u, delta, A, B, C, Dv, h_prev, out, h_last, ckpt, s, st);
+hipError_t launch_ssm_fwd(bool is_half, int spl, const FwdArgs& a, const SsmShape& s, hipStream_t st) {
+#define MWC_FWD_SPL(S) \
+    if (spl == S) return is_half ? fwd_inst<half_t, S>(a, s, st) : fwd_inst<float, S>(a, s, st);
     MWC_FWD_SPL(1)
     MWC_FWD_SPL(2)
     MWC_FWD_SPL(4)

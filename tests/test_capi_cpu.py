@@ -75,7 +75,10 @@ def test_workspace_sizes_monotone():
     a = L.mwc_ssm_bwd_workspace_size(8, 2048, 1536, 16)
     b = L.mwc_ssm_bwd_workspace_size(8, 4096, 1536, 16)
     assert 0 < a < b
-    assert L.mwc_ssm_fwd_workspace_size(8, 2048, 1536, 16) == 0  # the forward stages through LDS
+    # the forward needs workspace only for the carries of a split sequence
+    assert L.mwc_ssm_fwd_workspace_size(1, 16, 64, 16) == 0
+    assert L.mwc_ssm_fwd_workspace_size(8, 2048, 1536, 16) % 256 == 0
+    assert L.mwc_ssm_fwd_workspace_size(1, 131072, 2048, 16) > 0
     assert L.mwc_pscan_workspace_size(4, 65536, 1024) > 0
 
 

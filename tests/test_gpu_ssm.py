@@ -67,6 +67,51 @@ def test_forward_backward_parity(dev, shape, dtype, with_h):
         _close("dh_prev", g["h_prev"], r["dh_prev"], dtype)
 
 
+# Forced launch plans: states per lane x segments of L x carry segments per segment.
+PLANS = [(1, 1, 1), (1, 3, 1), (1, 4, 2), (2, 2, 1), (2, 5, 4), (4, 3, 2), (2, 64, 1)]
+
+
+@pytest.mark.parametrize("plan", PLANS)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_segmented_plans(dev, monkeypatch, plan, dtype):
+    """L split into segments (carry pass + main pass): same results as the oracle, incl. h_prev/dh_last."""
+    spl, nseg, cfold = plan
+    monkeypatch.setenv("MWC_SPL", str(spl))
+    monkeypatch.setenv("MWC_NSEG", str(nseg))
+    monkeypatch.setenv("MWC_CFOLD", str(cfold))
+    B, L, D = 2, 333, 200
+    print(f"case segmented plan={plan} dtype={dtype}", flush=True)
+    x = workloads.ssm_inputs(B, L, D, dtype=dtype, h_prev=True, seed=17 + nseg)
+    dhl = (0.5 * torch.randn(B, D, 16, generator=torch.Generator().manual_seed(4))).to(dtype)
+    out, h_last, g = _run(x, dev, with_h=True, dh_last=dhl)
+    ro, rh = orc.ssm_fwd(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["h_prev"], clamp=True)
+    _close("out", out, ro, dtype)
+    _close("h_last", h_last, rh, dtype)
+    r = orc.ssm_bwd(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["dout"], x["h_prev"], dhl, clamp=True)
+    for k, name in GRADS:
+        _close(name, g[k], r[name], dtype)
+    _close("dh_prev", g["h_prev"], r["dh_prev"], dtype)
+
+
+def test_segmented_clamp_path(dev, monkeypatch):
+    """Segments whose carries take the clamped exponent path (|delta*A| > 88 in some chunks)."""
+    monkeypatch.setenv("MWC_NSEG", "4")
+    monkeypatch.setenv("MWC_CFOLD", "2")
+    B, L, D = 1, 256, 64
+    x = workloads.ssm_inputs(B, L, D, dtype=torch.float32, h_prev=True, seed=23)
+    x["delta"][:, 40:60] *= 2000.0  # delta up to 200 with |A| up to 1: exponents beyond -88
+    x["delta"][:, 150:151] *= 5000.0
+    dhl = torch.randn(B, D, 16, generator=torch.Generator().manual_seed(5))
+    out, h_last, g = _run(x, dev, with_h=True, dh_last=dhl)
+    ro, rh = orc.ssm_fwd(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["h_prev"], clamp=True)
+    _close("out", out, ro, torch.float32)
+    _close("h_last", h_last, rh, torch.float32)
+    r = orc.ssm_bwd(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["dout"], x["h_prev"], dhl, clamp=True)
+    for k, name in GRADS:
+        _close(name, g[k], r[name], torch.float32)
+    _close("dh_prev", g["h_prev"], r["dh_prev"], torch.float32)
+
+
 def test_checkpoint_levels_agree_bitwise(dev):
     x = workloads.ssm_inputs(2, 300, 96, dtype=torch.float32, h_prev=True, seed=5)
     _, _, g0 = _run(x, dev, with_h=True, lvl=0)
@@ -120,7 +165,9 @@ def test_config2_training_step(dev):
 
 def test_streaming_equals_full_pass(dev):
     """Chunks carried through h_prev -> h_last reproduce one full pass (reference
-    tests/test_selective_scan.py:148-193), here in fp32 with config-2 distributions."""
+    tests/test_selective_scan.py:148-193, which bounds the max difference by 1e-3), here in fp32
+    with config-2 distributions. The full pass may split L into segments whose carries are
+    combined in a different order than the stream's, so the bound is rounding-level, not bitwise."""
     x = workloads.ssm_inputs(2, 1024, 256, dtype=torch.float32, seed=7, dout=False)
     xd = {k: v.to(dev) for k, v in x.items()}
     m = SelectiveScanCuda()
@@ -133,8 +180,8 @@ def test_streaming_equals_full_pass(dev):
             o, h = m.forward_with_state(xd["u"][:, sl], xd["delta"][:, sl], xd["A"], xd["B"][:, sl],
                                         xd["C"][:, sl], xd["D"], h)
             outs.append(o)
-    torch.testing.assert_close(torch.cat(outs, 1), full, rtol=1e-5, atol=1e-6)
-    torch.testing.assert_close(h, h_full, rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(torch.cat(outs, 1), full, rtol=1e-4, atol=1e-5)
+    torch.testing.assert_close(h, h_full, rtol=1e-4, atol=1e-5)
 
 
 def test_stateful_gradient_chain(dev):
@@ -256,7 +303,8 @@ def test_config4a_streaming_long_sequence(dev):
             outs.append(o[:, :, :256].cpu())
         full_out, full_h = m.forward_with_state(xd["u"], xd["delta"], xd["A"], xd["B"], xd["C"], xd["D"])
     torch.cuda.synchronize()
-    torch.testing.assert_close(h, full_h, rtol=1e-5, atol=1e-6)
+    # both passes may split L into segments at different points: agreement to the fp32 tolerance
+    torch.testing.assert_close(h, full_h, **TOL[torch.float32])
     ro, rh = orc.ssm_fwd(x["u"][:, :, :256], x["delta"][:, :, :256], x["A"][:256], x["B"], x["C"],
                          x["D"][:256], None, clamp=True)
     _close("h_last", h[:, :256], rh, torch.float32)
