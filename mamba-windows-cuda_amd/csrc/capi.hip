@@ -39,7 +39,7 @@ int check_dims(int dtype, int64_t batch, int64_t seqlen, int64_t dim, int64_t ds
     if (batch < 0 || seqlen < 0 || dim < 0)
         return fail(MWC_ERR_INVALID_ARGUMENT, "negative size (batch=%lld, seqlen=%lld, dim=%lld)", (long long)batch,
                     (long long)seqlen, (long long)dim);
-    if (seqlen > INT32_MAX / 2 || dim > INT32_MAX / 2 || batch > 65535)
+    if (seqlen > INT32_MAX / 2 || dim > (int64_t(1) << 24) || batch > 65535)
         return fail(MWC_ERR_UNSUPPORTED, "sizes beyond the supported range (batch=%lld, seqlen=%lld, dim=%lld)",
                     (long long)batch, (long long)seqlen, (long long)dim);
     return MWC_OK;
@@ -124,8 +124,8 @@ SegPlan plan(const SsmShape& s, bool bwd, int cap_main, int cap_carry, double ca
 
 // Workgroups per CU each kernel fits, by SPL: min(512 / VGPRs per lane, 160 KB / LDS per
 // workgroup), from the gfx950 build's resource usage.
-int fwd_cap(int spl) { return spl == 1 ? 4 : spl == 2 ? 3 : 1; }
-int fwd_carry_cap(int spl) { return spl == 1 ? 5 : spl == 2 ? 4 : 2; }
+int fwd_cap(int spl) { return spl == 1 ? 5 : spl == 2 ? 3 : 1; }
+int fwd_carry_cap(int spl) { return spl == 1 ? 6 : spl == 2 ? 4 : 2; }
 int bwd_cap(int spl) { return spl == 1 ? 3 : spl == 2 ? bwd_min_waves(2) : 1; }
 int bwd_carry_cap(int spl) { return spl == 1 ? 5 : spl == 2 ? 4 : 2; }
 

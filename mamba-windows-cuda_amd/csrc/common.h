@@ -23,6 +23,38 @@ __device__ __forceinline__ float exp2_clamped(float x2) {
     return __builtin_amdgcn_exp2f(__builtin_fminf(__builtin_fmaxf(x2, -kExp2Clamp), kExp2Clamp));
 }
 
+// Raw buffer access (gfx9 buffer resource, stride 0): a load whose byte offset is at or beyond the
+// resource's size returns 0 and such a store is dropped, so tails and padding lanes need no branches.
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9 dword 3: 32-bit data format, no swizzle
+constexpr uint32_t kOob = 0x80000000u;   // an offset past every resource built here (sizes < 2^31)
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcWord3);
+}
+template <typename T> __device__ __forceinline__ float buf_ld(rsrc_t r, uint32_t off);
+template <> __device__ __forceinline__ float buf_ld<float>(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+template <> __device__ __forceinline__ float buf_ld<half_t>(rsrc_t r, uint32_t off) {
+    return static_cast<float>(__builtin_bit_cast(half_t, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0)));
+}
+// Raw storage-type load (conversion deferred, keeps fp16 values in 16 bits while in flight).
+template <typename T> __device__ __forceinline__ T buf_raw(rsrc_t r, uint32_t off);
+template <> __device__ __forceinline__ float buf_raw<float>(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+template <> __device__ __forceinline__ half_t buf_raw<half_t>(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(half_t, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+}
+template <typename T> __device__ __forceinline__ void buf_st(rsrc_t r, uint32_t off, float v);
+template <> __device__ __forceinline__ void buf_st<float>(rsrc_t r, uint32_t off, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, v), r, off, 0, 0);
+}
+template <> __device__ __forceinline__ void buf_st<half_t>(rsrc_t r, uint32_t off, float v) {
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, static_cast<half_t>(v)), r, off, 0, 0);
+}
+
 // DPP lane exchanges within 16-lane rows (gfx9 DPP controls).
 template <int CTRL> __device__ __forceinline__ float dpp(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));

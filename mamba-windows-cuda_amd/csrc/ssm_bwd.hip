@@ -141,24 +141,28 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
         xs[j] = 0.f;
     }
 
+    // buffer resources per chunk: rows past L and channels past D read as 0 (see the main kernel)
+    const uint32_t lofs = lvalid ? ((uint32_t)(sg * SPG) * (uint32_t)D + (uint32_t)ld_d) * sizeof(T) : kOob;
+    const uint32_t row_bytes = (uint32_t)D * sizeof(T);
     T pd[SPG], py[SPG], pc;
     auto issue = [&](int k) {
+        const int64_t ck = (int64_t)k * TC;
+        const uint32_t rows = (uint32_t)min(TC, L - k * TC);
+        const rsrc_t rd = make_rsrc(delta + (row0 + ck) * D, rows * row_bytes);
+        const rsrc_t ry = make_rsrc(dout + (row0 + ck) * D, rows * row_bytes);
 #pragma unroll
         for (int s = 0; s < SPG; ++s) {
-            const int t = min(k * TC + sg * SPG + s, L - 1);
-            const int64_t off = (row0 + t) * D + ld_d;
-            pd[s] = delta[off];
-            py[s] = dout[off];
+            pd[s] = buf_raw<T>(rd, lofs + s * row_bytes);
+            py[s] = buf_raw<T>(ry, lofs + s * row_bytes);
         }
-        pc = Cm[(row0 + min(k * TC + bc_t, L - 1)) * kNState + bc_n];
+        pc = buf_raw<T>(make_rsrc(Cm + (row0 + ck) * kNState, rows * kNState * sizeof(T)), tid * sizeof(T));
     };
-    auto commit = [&](int k, int buf) {
+    auto commit = [&](int buf) {
         float vd[SPG], vy[SPG];
 #pragma unroll
         for (int s = 0; s < SPG; ++s) {
-            const bool ok = lvalid && (k * TC + sg * SPG + s < L);
-            vd[s] = ok ? static_cast<float>(pd[s]) : 0.f;
-            vy[s] = ok ? static_cast<float>(py[s]) : 0.f;
+            vd[s] = static_cast<float>(pd[s]);
+            vy[s] = static_cast<float>(py[s]);
         }
         stv<SPG>(&s_in[buf][0][lc][sg * SPG], vd);
         stv<SPG>(&s_in[buf][1][lc][sg * SPG], vy);
@@ -167,7 +171,7 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
 
     if (k0 < k1) {
         issue(k1 - 1);
-        commit(k1 - 1, (k1 - 1) & 1);
+        commit((k1 - 1) & 1);
     }
     __syncthreads();
     for (int k = k1 - 1; k >= k0; --k) {
@@ -208,7 +212,7 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
 #pragma unroll
             for (int j = 0; j < SPL; ++j) xs[j] = __builtin_fmaf(A2[j], sdt, xs[j]);
         }
-        if (more) commit(k - 1, buf ^ 1);
+        if (more) commit(buf ^ 1);
         __syncthreads();
     }
     if (valid) {
@@ -297,30 +301,38 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_mi
     const float Dd = ld(Dv + d);
     const float* ckb = ckpt + ((int64_t)b * nck * D + d) * kNState + n0;
 
+    // Chunk k's rows are read through buffer resources spanning exactly its min(16, L - 16k) rows:
+    // rows past L and channels past D (offset kOob) read as 0 and their stores are dropped.
+    const uint32_t lofs = lvalid ? ((uint32_t)(sg * SPG) * (uint32_t)D + (uint32_t)ld_d) * sizeof(T) : kOob;
+    const uint32_t row_bytes = (uint32_t)D * sizeof(T);
+    auto chunk_rows = [&](int k) { return (uint32_t)min(TC, L - k * TC); };
+    const int64_t rowD = row0 * D;
     T pu[SPG], pd[SPG], py[SPG], pb, pc;
     float hnext[SPL];
     auto issue = [&](int k) {
+        const int64_t ck = (int64_t)k * TC;
+        const uint32_t rows = chunk_rows(k);
+        const rsrc_t ru = make_rsrc(u + rowD + ck * D, rows * row_bytes);
+        const rsrc_t rd = make_rsrc(delta + rowD + ck * D, rows * row_bytes);
+        const rsrc_t ry = make_rsrc(dout + rowD + ck * D, rows * row_bytes);
 #pragma unroll
         for (int s = 0; s < SPG; ++s) {
-            const int t = min(k * TC + sg * SPG + s, L - 1);
-            const int64_t off = (row0 + t) * D + ld_d;
-            pu[s] = u[off];
-            pd[s] = delta[off];
-            py[s] = dout[off];
+            pu[s] = buf_raw<T>(ru, lofs + s * row_bytes);
+            pd[s] = buf_raw<T>(rd, lofs + s * row_bytes);
+            py[s] = buf_raw<T>(ry, lofs + s * row_bytes);
         }
-        const int t = min(k * TC + bc_t, L - 1);
-        pb = Bm[(row0 + t) * kNState + bc_n];
-        pc = Cm[(row0 + t) * kNState + bc_n];
+        const uint32_t bc_bytes = rows * kNState * sizeof(T);
+        pb = buf_raw<T>(make_rsrc(Bm + (row0 + ck) * kNState, bc_bytes), tid * sizeof(T));
+        pc = buf_raw<T>(make_rsrc(Cm + (row0 + ck) * kNState, bc_bytes), tid * sizeof(T));
         ldv<SPL>(ckb + (int64_t)k * D * kNState, hnext);
     };
-    auto commit = [&](int k) {
+    auto commit = [&]() {
         float vd[SPG], vdu[SPG], vu[SPG], vy[SPG];
 #pragma unroll
         for (int s = 0; s < SPG; ++s) {
-            const bool ok = lvalid && (k * TC + sg * SPG + s < L);
-            vd[s] = ok ? static_cast<float>(pd[s]) : 0.f;
-            vu[s] = ok ? static_cast<float>(pu[s]) : 0.f;
-            vy[s] = ok ? static_cast<float>(py[s]) : 0.f;
+            vd[s] = static_cast<float>(pd[s]);
+            vu[s] = static_cast<float>(pu[s]);
+            vy[s] = static_cast<float>(py[s]);
             vdu[s] = vd[s] * vu[s];
         }
         stv<SPG>((s_in(0, lc) + sg * SPG), vd);
@@ -334,7 +346,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_mi
     float hin[SPL];
     if (k0 < k1) {  // L == 0 has no chunk; the outputs below are then dh_prev = dh_last and zero partials
         issue(k1 - 1);
-        commit(k1 - 1);
+        commit();
 #pragma unroll
         for (int j = 0; j < SPL; ++j) hin[j] = hnext[j];
     }
@@ -443,10 +455,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_mi
                 const float prev = (i > 0) ? H[i > 0 ? i - 1 : 0][j] : hin[j];
                 gt[j] = __builtin_fmaf(yo, Cv[j], gc[j]);
                 r1 = __builtin_fmaf(gt[j], Bv[j], r1);
-                const float s = gt[j] * E[i][j] * prev;
+                gc[j] = E[i][j] * gt[j];
+                const float s = gc[j] * prev;  // g * dA_t * h_{t-1}
                 r2 = __builtin_fmaf(An[j], s, r2);
                 dAacc[j] = __builtin_fmaf(dt[i], s, dAacc[j]);
-                gc[j] = E[i][j] * gt[j];
             }
             r1 = group_sum<LPC>(r1);
             r2 = group_sum<LPC>(r2);
@@ -465,27 +477,18 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_mi
         }
         __syncthreads();  // every wave is done with the staged chunk and has written s_out / s_part
         if (more) {
-            commit(k - 1);
+            commit();
 #pragma unroll
             for (int j = 0; j < SPL; ++j) hin[j] = hnext[j];
         }
-        // coalesced du / ddelta tile stores: thread -> (step, VPT channels)
+        // du / ddelta of the loader's (channel, steps), read back from the tile
         {
-            constexpr int VPT = CPB / 16;
-            const int sr = tid >> 4, cq = (tid & 15) * VPT;
-            const int t = t0 + sr;
-            if (t < L) {
-                float a[VPT], bb[VPT];
-                ldv<VPT>(&s_out[0][sr][cq], a);
-                ldv<VPT>(&s_out[1][sr][cq], bb);
-                T* pdu = du + (row0 + t) * D + d0 + cq;
-                T* pdd = ddelta + (row0 + t) * D + d0 + cq;
+            const rsrc_t rdu = make_rsrc(du + rowD + (int64_t)t0 * D, chunk_rows(k) * row_bytes);
+            const rsrc_t rdd = make_rsrc(ddelta + rowD + (int64_t)t0 * D, chunk_rows(k) * row_bytes);
 #pragma unroll
-                for (int q = 0; q < VPT; ++q)
-                    if (d0 + cq + q < D) {
-                        pdu[q] = static_cast<T>(a[q]);
-                        pdd[q] = static_cast<T>(bb[q]);
-                    }
+            for (int s = 0; s < SPG; ++s) {
+                buf_st<T>(rdu, lofs + s * row_bytes, s_out[0][sg * SPG + s][lc]);
+                buf_st<T>(rdd, lofs + s * row_bytes, s_out[1][sg * SPG + s][lc]);
             }
         }
         // this workgroup's dB/dC partial for the chunk (sum of its 4 waves)

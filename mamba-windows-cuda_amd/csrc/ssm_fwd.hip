@@ -88,11 +88,10 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
     constexpr int RS = TC + 4;          // LDS row stride (floats) of a channel's steps
     constexpr int NSG = 256 / CPB;      // loader step groups
     constexpr int SPG = TC / NSG;       // steps per loader thread
-    constexpr int YS = CPB + 4;         // LDS row stride of the output tile
-    constexpr int NPL = HAS_OUT ? 3 : 2;
+    constexpr int YS = CPB + 4;         // LDS row stride of the output tile (16 mod 64 banks apart)
     static_assert(NSG * SPG == TC, "loader tiling");
 
-    __shared__ float s_in[2][NPL][CPB][RS];  // [buf][delta, delta*u, u][channel][step]
+    __shared__ float s_in[2][2][CPB][RS];  // [buf][delta, delta*u][channel][step]
     __shared__ float s_bc[2][TC][HAS_OUT ? 2 * kNState : kNState];
     __shared__ float s_y[HAS_OUT ? 2 : 1][HAS_OUT ? TC : 1][HAS_OUT ? YS : 1];
 
@@ -141,55 +140,68 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
             for (int q = 0; q < SPL; ++q) h[q] = __builtin_fmaf(__builtin_amdgcn_exp2f(cx[q]), h[q], ch[q]);
         }
     }
-    const float Dd = ld(Dv + d);
-
+    // Chunk k's rows are read through buffer resources spanning exactly its min(16, L - 16k) rows:
+    // rows past L and channels past D (offset kOob) read as 0, which is the padding the scan needs.
+    const T* ub = u + row0 * D;
+    const T* db = delta + row0 * D;
+    const T* Bb = Bm + row0 * kNState;
+    const T* Cb = Cm + row0 * kNState;
+    const uint32_t lofs = lvalid ? ((uint32_t)(sg * SPG) * (uint32_t)D + (uint32_t)ld_d) * sizeof(T) : kOob;
+    const uint32_t row_bytes = (uint32_t)D * sizeof(T);
+    auto chunk_rows = [&](int k) { return (uint32_t)min(TC, L - k * TC); };
     T pu[SPG], pd[SPG], pb, pc;
     auto issue = [&](int k) {
+        const int64_t ck = (int64_t)k * TC;
+        const uint32_t rows = chunk_rows(k);
+        const rsrc_t ru = make_rsrc(ub + ck * D, rows * row_bytes);
+        const rsrc_t rd = make_rsrc(db + ck * D, rows * row_bytes);
 #pragma unroll
         for (int s = 0; s < SPG; ++s) {
-            const int t = min(k * TC + sg * SPG + s, L - 1);
-            const int64_t off = (row0 + t) * D + ld_d;
-            pu[s] = u[off];
-            pd[s] = delta[off];
+            pu[s] = buf_raw<T>(ru, lofs + s * row_bytes);
+            pd[s] = buf_raw<T>(rd, lofs + s * row_bytes);
         }
-        const int t = min(k * TC + bc_t, L - 1);
-        pb = Bm[(row0 + t) * kNState + bc_n];
-        if constexpr (HAS_OUT) pc = Cm[(row0 + t) * kNState + bc_n];
+        pb = buf_raw<T>(make_rsrc(Bb + ck * kNState, rows * kNState * sizeof(T)), tid * sizeof(T));
+        if constexpr (HAS_OUT) pc = buf_raw<T>(make_rsrc(Cb + ck * kNState, rows * kNState * sizeof(T)), tid * sizeof(T));
     };
-    auto commit = [&](int k, int buf) {
-        float vd[SPG], vdu[SPG], vu[SPG];
+    // D*u of the loader's (channel, steps) for the chunk being computed and the next one; the
+    // loader thread also stores those outputs, so the consumer lanes never touch u
+    const float Dl = HAS_OUT ? ld(Dv + ld_d) : 0.f;
+    float du_cur[SPG], du_nxt[SPG];
+    auto commit = [&](int buf) {
+        float vd[SPG], vdu[SPG];
 #pragma unroll
         for (int s = 0; s < SPG; ++s) {
-            const bool ok = lvalid && (k * TC + sg * SPG + s < L);
-            vd[s] = ok ? static_cast<float>(pd[s]) : 0.f;
-            vu[s] = ok ? static_cast<float>(pu[s]) : 0.f;
-            vdu[s] = vd[s] * vu[s];
+            vd[s] = static_cast<float>(pd[s]);
+            const float vu = static_cast<float>(pu[s]);
+            vdu[s] = vd[s] * vu;
+            du_nxt[s] = Dl * vu;
         }
         vst<SPG>(&s_in[buf][0][lc][sg * SPG], vd);
         vst<SPG>(&s_in[buf][1][lc][sg * SPG], vdu);
-        if constexpr (HAS_OUT) vst<SPG>(&s_in[buf][2][lc][sg * SPG], vu);
         s_bc[buf][bc_t][bc_n] = static_cast<float>(pb);
         if constexpr (HAS_OUT) s_bc[buf][bc_t][kNState + bc_n] = static_cast<float>(pc);
     };
 
     if (k0 < k1) {  // every segment holds a chunk unless L == 0 (then h_last = h_prev)
         issue(k0);
-        commit(k0, k0 & 1);
+        commit(k0 & 1);
     }
     __syncthreads();
     float* ckb = (!CARRY && ckpt) ? ckpt + ((int64_t)b * nck * D + d) * kNState + n0 : nullptr;
+    T* ob = HAS_OUT ? out + row0 * D : nullptr;
 
     for (int k = k0; k < k1; ++k) {
         const int buf = k & 1;
         const bool more = k + 1 < k1;
+#pragma unroll
+        for (int s = 0; s < SPG; ++s) du_cur[s] = du_nxt[s];
         if (more) issue(k + 1);
         if (ckb != nullptr && valid) vst<SPL>(ckb + (int64_t)k * D * kNState, h);
 
         // the whole chunk's operands, read up front so LDS latency is paid once per chunk
-        float dt[TC], dtu[TC], uu[TC], Bv[TC][SPL], Cv[TC][SPL];
+        float dt[TC], dtu[TC], Bv[TC][SPL], Cv[TC][SPL];
         lds_ld<TC>(&s_in[buf][0][c][0], dt);
         lds_ld<TC>(&s_in[buf][1][c][0], dtu);
-        if constexpr (HAS_OUT) lds_ld<TC>(&s_in[buf][2][c][0], uu);
 #pragma unroll
         for (int i = 0; i < TC; ++i) {
             lds_ld<SPL>(&s_bc[buf][i][n0], Bv[i]);
@@ -216,9 +228,8 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
                     if constexpr (HAS_OUT) y = __builtin_fmaf(Cv[i][j], h[j], y);
                 }
                 if constexpr (HAS_OUT) {
-                    y = group_sum<LPC>(y);
                     // every lane of the group holds the sum; the duplicate LDS writes are identical
-                    s_y[buf][i][c] = __builtin_fmaf(Dd, uu[i], y);
+                    s_y[buf][i][c] = group_sum<LPC>(y);
                 }
             }
         };
@@ -234,21 +245,13 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
                 for (int j = 0; j < SPL; ++j) xs[j] = __builtin_fmaf(A2[j], sdt, xs[j]);
             }
         }
-        if (more) commit(k + 1, buf ^ 1);
+        if (more) commit(buf ^ 1);
         __syncthreads();
         if constexpr (HAS_OUT) {
-            // coalesced store of the chunk's output tile: thread -> (step, VPT channels)
-            constexpr int VPT = CPB / (256 / TC);
-            const int sr = tid / (CPB / VPT), cq = (tid % (CPB / VPT)) * VPT;
-            const int t = k * TC + sr;
-            if (t < L) {
-                float v[VPT];
-                lds_ld<VPT>(&s_y[buf][sr][cq], v);
-                T* op = out + (row0 + t) * D + d0 + cq;
+            // the loader's (channel, steps) outputs: y from the tile plus D*u
+            const rsrc_t ro = make_rsrc(ob + (int64_t)k * TC * D, chunk_rows(k) * row_bytes);
 #pragma unroll
-                for (int q = 0; q < VPT; ++q)
-                    if (d0 + cq + q < D) op[q] = static_cast<T>(v[q]);
-            }
+            for (int s = 0; s < SPG; ++s) buf_st<T>(ro, lofs + s * row_bytes, s_y[buf][sg * SPG + s][lc] + du_cur[s]);
         }
     }
     if constexpr (CARRY) {
