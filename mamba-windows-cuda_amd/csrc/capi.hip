@@ -95,8 +95,7 @@ int cpb_of(int spl) { return 4 * 64 / (kNState / spl); }
 // Picks the segment count (and the carry split) minimising the modelled time of
 // carry pass + main pass. caps = workgroups per CU each kernel fits (registers, LDS);
 // carry_rel = cost of a carry-pass chunk relative to a main-pass chunk.
-SegPlan plan(const SsmShape& s, bool bwd, int cap_main, int cap_carry, double carry_rel) {
-    const int spl = choose_spl(s.batch * s.dim);
+SegPlan plan(const SsmShape& s, bool bwd, int spl, int cap_main, int cap_carry, double carry_rel) {
     const int64_t nck = (s.seqlen + kCkptSteps - 1) / kCkptSteps;
     const int64_t w1 = s.batch * ((s.dim + cpb_of(spl) - 1) / cpb_of(spl));
     SegPlan best{spl, 1, (int)nck, 1, 0};
@@ -126,7 +125,7 @@ SegPlan plan(const SsmShape& s, bool bwd, int cap_main, int cap_carry, double ca
 // workgroup), from the gfx950 build's resource usage.
 int fwd_cap(int spl) { return spl == 1 ? 5 : spl == 2 ? 3 : 1; }
 int fwd_carry_cap(int spl) { return spl == 1 ? 6 : spl == 2 ? 4 : 2; }
-int bwd_cap(int spl) { return spl == 1 ? 3 : spl == 2 ? bwd_min_waves(2) : 1; }
+int bwd_cap(int spl) { return spl == 4 ? 1 : 3; }
 int bwd_carry_cap(int spl) { return spl == 1 ? 5 : spl == 2 ? 4 : 2; }
 
 size_t carry_bytes(const SsmShape& s, const SegPlan& p) {
@@ -137,12 +136,12 @@ size_t carry_bytes(const SsmShape& s, const SegPlan& p) {
 
 SegPlan plan_fwd(const SsmShape& s) {
     const int spl = choose_spl(s.batch * s.dim);
-    return plan(s, false, fwd_cap(spl), fwd_carry_cap(spl), 0.6);
+    return plan(s, false, spl, fwd_cap(spl), fwd_carry_cap(spl), 0.6);
 }
 
 SegPlan plan_bwd(const SsmShape& s) {
     const int spl = choose_spl(s.batch * s.dim);
-    return plan(s, true, bwd_cap(spl), bwd_carry_cap(spl), 0.3);
+    return plan(s, true, spl, bwd_cap(spl), bwd_carry_cap(spl), 0.3);
 }
 
 // Kernel family: 2 = lane groups (ssm_fwd.hip / ssm_bwd.hip, the default), 3 = state groups across

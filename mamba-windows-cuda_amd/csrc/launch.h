@@ -10,13 +10,8 @@ struct SsmShape {
 };
 
 // Waves per SIMD the lane-group kernels are compiled to fit (each lane then has 512/W VGPRs).
-// The backward at SPL=2 needs ~200 VGPRs for its chunk of recomputed states; squeezed to 3 waves
-// it spills (the build option MWC_BWD_SPL2_WAVES selects 2 or 3).
-#ifndef MWC_BWD_SPL2_WAVES
-#define MWC_BWD_SPL2_WAVES 2
-#endif
 constexpr int fwd_min_waves(int spl) { return spl == 4 ? 1 : 3; }
-constexpr int bwd_min_waves(int spl) { return spl == 4 ? 1 : spl == 2 ? MWC_BWD_SPL2_WAVES : 3; }
+constexpr int bwd_min_waves(int spl) { return spl == 4 ? 1 : 3; }
 
 // Launch plan of the lane-group kernels: SPL = states held per lane (16/SPL lanes per channel),
 // nseg = segments L is cut into (cps chunks of kCkptSteps steps each), cfold = carry segments per

@@ -223,7 +223,8 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
 }
 
 template <typename T, int SPL>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_min_waves(SPL), 8))) ssm_bwd_kernel(
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_min_waves(SPL), 8)))
+ssm_bwd_kernel(
     const T* __restrict__ u, const T* __restrict__ delta, const T* __restrict__ A, const T* __restrict__ Bm,
     const T* __restrict__ Cm, const T* __restrict__ Dv, const T* __restrict__ dout, const T* __restrict__ dh_last,
     const float* __restrict__ ckpt, T* __restrict__ du, T* __restrict__ ddelta, T* __restrict__ dh_prev,
@@ -253,6 +254,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_mi
     auto s_in = [&](int plane, int ch) -> float* { return &s_in_raw[plane * AS + ch * RS]; };
     __shared__ float s_part[4][TC][2 * kNState];
     __shared__ float s_out[2][TC][OS];  // [du, ddelta][step][channel]
+    __shared__ int s_flag;              // index of the last staged chunk that needs the exponent clamp
 
     const int tid = threadIdx.x;
     const int lid = xcd_remap(blockIdx.x, gridDim.x);
@@ -326,15 +328,22 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_mi
         pc = buf_raw<T>(make_rsrc(Cm + (row0 + ck) * kNState, bc_bytes), tid * sizeof(T));
         ldv<SPL>(ckb + (int64_t)k * D * kNState, hnext);
     };
-    auto commit = [&]() {
+    float lamax2 = 0.f;  // max_n |A[ld_d][n]| * log2(e): the loader flags chunks that reach the clamp
+#pragma unroll
+    for (int n = 0; n < kNState; ++n) lamax2 = __builtin_fmaxf(lamax2, __builtin_fabsf(ld(A + (int64_t)ld_d * kNState + n)));
+    lamax2 *= kLog2e;
+    auto commit = [&](int k) {
         float vd[SPG], vdu[SPG], vu[SPG], vy[SPG];
+        float vmax = 0.f;
 #pragma unroll
         for (int s = 0; s < SPG; ++s) {
             vd[s] = static_cast<float>(pd[s]);
             vu[s] = static_cast<float>(pu[s]);
             vy[s] = static_cast<float>(py[s]);
             vdu[s] = vd[s] * vu[s];
+            vmax = __builtin_fmaxf(vmax, __builtin_fabsf(vd[s]));
         }
+        if (vmax * lamax2 > kExp2Clamp) s_flag = k;  // benign race: every writer stores k
         stv<SPG>((s_in(0, lc) + sg * SPG), vd);
         stv<SPG>((s_in(1, lc) + sg * SPG), vdu);
         stv<SPG>((s_in(2, lc) + sg * SPG), vu);
@@ -344,9 +353,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_mi
     };
 
     float hin[SPL];
+    if (tid == 0) s_flag = -1;
+    __syncthreads();
     if (k0 < k1) {  // L == 0 has no chunk; the outputs below are then dh_prev = dh_last and zero partials
         issue(k1 - 1);
-        commit();
+        commit(k1 - 1);
 #pragma unroll
         for (int j = 0; j < SPL; ++j) hin[j] = hnext[j];
     }
@@ -354,40 +365,41 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_mi
 
     float* red_g = &s_red[wave][0];   // [slot][channel][16]
     float* red_h = &s_red[wave][PL];  // [slot][channel][16]
-    float amax2 = 0.f;
-#pragma unroll
-    for (int j = 0; j < SPL; ++j) amax2 = __builtin_fmaxf(amax2, __builtin_fabsf(A2[j]));
 
     for (int k = k1 - 1; k >= k0; --k) {
         const int t0 = k * TC;
         const bool more = k > k0;
         if (more) issue(k - 1);
+        // one workgroup-uniform decision per chunk: the clamped path gives the same values whenever
+        // no exponent reaches the clamp, so deciding for the whole workgroup is exact
+        const bool need_clamp = __builtin_amdgcn_readfirstlane(s_flag) == k;
 
-        // ---- recompute the chunk's states (one exp per state) ----
-        float H[TC][SPL], E[TC][SPL], dt[TC];
+        // ---- recompute the chunk's states (one exp per state), 4 steps per operand read ----
+        float H[TC][SPL], E[TC][SPL];
         {
-            float dtu[TC];
-            ldv<TC>(s_in(0, c), dt);
-            ldv<TC>(s_in(1, c), dtu);
-            float dmax = 0.f;
-#pragma unroll
-            for (int i = 0; i < TC; ++i) dmax = __builtin_fmaxf(dmax, __builtin_fabsf(dt[i]));
-            const bool need_clamp = __builtin_amdgcn_ballot_w64(dmax * amax2 > kExp2Clamp) != 0;
             auto recompute = [&](auto clamp_tag) {
                 constexpr bool CLAMP = decltype(clamp_tag)::value;
                 float hh[SPL];
 #pragma unroll
                 for (int j = 0; j < SPL; ++j) hh[j] = hin[j];
 #pragma unroll
-                for (int i = 0; i < TC; ++i) {
-                    float Bv[SPL];
-                    ldv<SPL>(&s_bc[i][n0], Bv);
+                for (int i4 = 0; i4 < TC; i4 += 4) {
+                    float dt4[4], dtu4[4];
+                    ldv<4>(s_in(0, c) + i4, dt4);
+                    ldv<4>(s_in(1, c) + i4, dtu4);
 #pragma unroll
-                    for (int j = 0; j < SPL; ++j) {
-                        const float x = dt[i] * A2[j];
-                        E[i][j] = CLAMP ? exp2_clamped(x) : __builtin_amdgcn_exp2f(x);
-                        hh[j] = __builtin_fmaf(E[i][j], hh[j], dtu[i] * Bv[j]);
-                        H[i][j] = hh[j];
+                    for (int q = 0; q < 4; ++q) {
+                        const int i = i4 + q;
+                        float Bv[SPL];
+                        ldv<SPL>(&s_bc[i][n0], Bv);
+#pragma unroll
+                        for (int j = 0; j < SPL; ++j) {
+                            const float x = dt4[q] * A2[j];
+                            const float e = CLAMP ? exp2_clamped(x) : __builtin_amdgcn_exp2f(x);
+                            E[i][j] = e;
+                            hh[j] = __builtin_fmaf(e, hh[j], dtu4[q] * Bv[j]);
+                            H[i][j] = hh[j];
+                        }
                     }
                 }
             };
@@ -418,66 +430,71 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_mi
             for (int q = 0; q < 4; ++q) acc[q] += dpp<kDppXor1>(acc[q]);
             if (rhalf == 0) stv<4>(&s_part[wave][phase * kRedSlots + rs][rq * 4], acc);
         };
-        float uq[4], yq[4], uqn[4], yqn[4], Bn[SPL], Cn[SPL];
-        ldv<4>(s_in(2, c) + TC - 4, uqn);
-        ldv<4>(s_in(3, c) + TC - 4, yqn);
-        ldv<SPL>(&s_bc[TC - 1][n0], Bn);
-        ldv<SPL>(&s_bc[TC - 1][kNState + n0], Cn);
+        {
+            float uq[4], yq[4], dq[4], uqn[4], yqn[4], dqn[4], Bn[SPL], Cn[SPL];
+            ldv<4>(s_in(2, c) + TC - 4, uqn);
+            ldv<4>(s_in(3, c) + TC - 4, yqn);
+            ldv<4>(s_in(0, c) + TC - 4, dqn);
+            ldv<SPL>(&s_bc[TC - 1][n0], Bn);
+            ldv<SPL>(&s_bc[TC - 1][kNState + n0], Cn);
 #pragma unroll
-        for (int i = TC - 1; i >= 0; --i) {
-            const int slot = i % kRedSlots, phase = i / kRedSlots;
-            if (slot == kRedSlots - 1) {
+            for (int i = TC - 1; i >= 0; --i) {
+                const int slot = i % kRedSlots, phase = i / kRedSlots;
+                if (slot == kRedSlots - 1) {
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    uq[q] = uqn[q];
-                    yq[q] = yqn[q];
+                    for (int q = 0; q < 4; ++q) {
+                        uq[q] = uqn[q];
+                        yq[q] = yqn[q];
+                        dq[q] = dqn[q];
+                    }
+                    if (i >= 4) {
+                        ldv<4>(s_in(2, c) + i - 7, uqn);
+                        ldv<4>(s_in(3, c) + i - 7, yqn);
+                        ldv<4>(s_in(0, c) + i - 7, dqn);
+                    }
                 }
-                if (i >= 4) {
-                    ldv<4>(s_in(2, c) + i - 7, uqn);
-                    ldv<4>(s_in(3, c) + i - 7, yqn);
+                float Bv[SPL], Cv[SPL];
+#pragma unroll
+                for (int j = 0; j < SPL; ++j) {
+                    Bv[j] = Bn[j];
+                    Cv[j] = Cn[j];
                 }
-            }
-            float Bv[SPL], Cv[SPL];
+                if (i > 0) {
+                    ldv<SPL>(&s_bc[i > 0 ? i - 1 : 0][n0], Bn);
+                    ldv<SPL>(&s_bc[i > 0 ? i - 1 : 0][kNState + n0], Cn);
+                }
+                const float ui = uq[slot], yo = yq[slot], dti = dq[slot];
+                float gt[SPL];
+                float r1 = 0.f, r2 = 0.f;
 #pragma unroll
-            for (int j = 0; j < SPL; ++j) {
-                Bv[j] = Bn[j];
-                Cv[j] = Cn[j];
-            }
-            if (i > 0) {
-                ldv<SPL>(&s_bc[i > 0 ? i - 1 : 0][n0], Bn);
-                ldv<SPL>(&s_bc[i > 0 ? i - 1 : 0][kNState + n0], Cn);
-            }
-            const float ui = uq[slot], yo = yq[slot];
-            float gt[SPL];
-            float r1 = 0.f, r2 = 0.f;
-#pragma unroll
-            for (int j = 0; j < SPL; ++j) {
-                const float prev = (i > 0) ? H[i > 0 ? i - 1 : 0][j] : hin[j];
-                gt[j] = __builtin_fmaf(yo, Cv[j], gc[j]);
-                r1 = __builtin_fmaf(gt[j], Bv[j], r1);
-                gc[j] = E[i][j] * gt[j];
-                const float s = gc[j] * prev;  // g * dA_t * h_{t-1}
-                r2 = __builtin_fmaf(An[j], s, r2);
-                dAacc[j] = __builtin_fmaf(dt[i], s, dAacc[j]);
-            }
-            r1 = group_sum<LPC>(r1);
-            r2 = group_sum<LPC>(r2);
-            // every lane of the group holds the sums; duplicate LDS writes are identical
-            s_out[0][i][c] = __builtin_fmaf(Dd, yo, dt[i] * r1);
-            s_out[1][i][c] = __builtin_fmaf(ui, r1, r2);
-            dDacc = __builtin_fmaf(yo, ui, dDacc);
-            const int sl = slot * CPW + cw;
-            stv<SPL>(red_g + sl * kNState + n0, gt);
-            stv<SPL>(red_h + sl * kNState + n0, H[i]);
-            if (slot == 0) {
-                wave_lds_fence();
-                fold(phase);
-                wave_lds_fence();
+                for (int j = 0; j < SPL; ++j) {
+                    const float prev = (i > 0) ? H[i > 0 ? i - 1 : 0][j] : hin[j];
+                    gt[j] = __builtin_fmaf(yo, Cv[j], gc[j]);
+                    r1 = __builtin_fmaf(gt[j], Bv[j], r1);
+                    gc[j] = E[i][j] * gt[j];
+                    const float s = gc[j] * prev;  // g * dA_t * h_{t-1}
+                    r2 = __builtin_fmaf(An[j], s, r2);
+                    dAacc[j] = __builtin_fmaf(dti, s, dAacc[j]);
+                }
+                r1 = group_sum<LPC>(r1);
+                r2 = group_sum<LPC>(r2);
+                // every lane of the group holds the sums; duplicate LDS writes are identical
+                s_out[0][i][c] = __builtin_fmaf(Dd, yo, dti * r1);
+                s_out[1][i][c] = __builtin_fmaf(ui, r1, r2);
+                dDacc = __builtin_fmaf(yo, ui, dDacc);
+                const int sl = slot * CPW + cw;
+                stv<SPL>(red_g + sl * kNState + n0, gt);
+                stv<SPL>(red_h + sl * kNState + n0, H[i]);
+                if (slot == 0) {
+                    wave_lds_fence();
+                    fold(phase);
+                    wave_lds_fence();
+                }
             }
         }
         __syncthreads();  // every wave is done with the staged chunk and has written s_out / s_part
         if (more) {
-            commit();
+            commit(k - 1);
 #pragma unroll
             for (int j = 0; j < SPL; ++j) hin[j] = hnext[j];
         }
