@@ -463,6 +463,9 @@ ssm_bwd_kernel(
                     ldv<SPL>(&s_bc[i > 0 ? i - 1 : 0][n0], Bn);
                     ldv<SPL>(&s_bc[i > 0 ? i - 1 : 0][kNState + n0], Cn);
                 }
+                // keep the next step's operand reads here, a full step ahead of their use (the
+                // scheduler would otherwise sink them next to the use and expose the LDS latency)
+                __builtin_amdgcn_sched_barrier(0);
                 const float ui = uq[slot], yo = yq[slot], dti = dq[slot];
                 float gt[SPL];
                 float r1 = 0.f, r2 = 0.f;
