@@ -531,28 +531,49 @@ ssm_bwd_kernel(
     }
 }
 
-// dB/dC: sum the channel-group partials in group order and cast.
+// The backward's reductions, one launch: blocks [0, nblk_bc) sum the channel-group dB/dC partials
+// (4 consecutive values per thread, groups in order), the rest sum the (segment, batch) dA/dD
+// partials in order. Fixed summation orders: the results are deterministic.
 template <typename T>
-__global__ void __launch_bounds__(256) bwd_finish_bc_kernel(const float* __restrict__ part, T* __restrict__ dB,
-                                                            T* __restrict__ dC, int ngrp, int64_t rows) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // over rows*32
-    if (i >= rows * 32) return;
-    float s = 0.f;
-    for (int q = 0; q < ngrp; ++q) s += part[(int64_t)q * rows * 32 + i];
-    const int64_t r = i >> 5;
-    const int v = (int)(i & 31);
-    if (v < kNState)
-        st(dB + r * kNState + v, s);
-    else
-        st(dC + r * kNState + v - kNState, s);
-}
-
-// dA (D,N) and dD (D,): sum the nrows (segment, batch) partials in order and cast.
-template <typename T>
-__global__ void __launch_bounds__(256) bwd_finish_ad_kernel(const float* __restrict__ dA_part,
-                                                            const float* __restrict__ dD_part, T* __restrict__ dA,
-                                                            T* __restrict__ dD, int nrows, int D) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+__global__ void __launch_bounds__(256) bwd_finish_kernel(const float* __restrict__ part, T* __restrict__ dB,
+                                                         T* __restrict__ dC, int ngrp, int64_t rows, int nblk_bc,
+                                                         const float* __restrict__ dA_part,
+                                                         const float* __restrict__ dD_part, T* __restrict__ dA,
+                                                         T* __restrict__ dD, int nrows, int D) {
+    if ((int)blockIdx.x < nblk_bc) {
+        const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;  // over rows*32, 4-aligned
+        if (i >= rows * 32) return;
+        const int64_t stride = rows * 32;
+        const float* p = part + i;
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        int q = 0;
+        for (; q + 4 <= ngrp; q += 4) {
+            float4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const float4*>(p + (int64_t)(q + u) * stride);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                acc[0] += v[u].x;
+                acc[1] += v[u].y;
+                acc[2] += v[u].z;
+                acc[3] += v[u].w;
+            }
+        }
+        for (; q < ngrp; ++q) {
+            const float4 v = *reinterpret_cast<const float4*>(p + (int64_t)q * stride);
+            acc[0] += v.x;
+            acc[1] += v.y;
+            acc[2] += v.z;
+            acc[3] += v.w;
+        }
+        const int64_t r = i >> 5;
+        const int col = (int)(i & 31);  // the 4 values are all dB (col < 16) or all dC
+        T* dst = col < kNState ? dB + r * kNState + col : dC + r * kNState + col - kNState;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) st(dst + u, acc[u]);
+        return;
+    }
+    const int64_t i = (int64_t)(blockIdx.x - nblk_bc) * 256 + threadIdx.x;
     const int64_t nA = (int64_t)D * kNState;
     if (i < nA) {
         float s = 0.f;
@@ -602,13 +623,11 @@ template <typename T>
 static hipError_t finish_t(const float* dbc_part, const float* dA_part, const float* dD_part, void* dB, void* dC,
                            void* dA, void* dD, int ngrp, int nrows, const SsmShape& s, hipStream_t st) {
     const int64_t rows = s.batch * s.seqlen;
-    const int g1 = (int)((rows * 32 + 255) / 256);
-    if (g1 > 0)
-        hipLaunchKernelGGL(bwd_finish_bc_kernel<T>, dim3(g1), dim3(256), 0, st, dbc_part, (T*)dB, (T*)dC, ngrp, rows);
+    const int nblk_bc = (int)((rows * 32 / 4 + 255) / 256);
     const int64_t n2 = s.dim * kNState + s.dim;
-    const int g2 = (int)((n2 + 255) / 256);
-    hipLaunchKernelGGL(bwd_finish_ad_kernel<T>, dim3(g2), dim3(256), 0, st, dA_part, dD_part, (T*)dA, (T*)dD, nrows,
-                       (int)s.dim);
+    const int nblk_ad = (int)((n2 + 255) / 256);
+    hipLaunchKernelGGL(bwd_finish_kernel<T>, dim3(nblk_bc + nblk_ad), dim3(256), 0, st, dbc_part, (T*)dB, (T*)dC,
+                       ngrp, rows, nblk_bc, dA_part, dD_part, (T*)dA, (T*)dD, nrows, (int)s.dim);
     return hipGetLastError();
 }
 
