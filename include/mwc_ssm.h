@@ -63,7 +63,8 @@ const char* mwc_last_error(void);
 /* Number of checkpoints for a sequence of `seqlen` steps: ceil(seqlen / MWC_CKPT_STEPS). */
 int64_t mwc_ssm_ckpt_count(int64_t seqlen);
 
-/* Workspace bytes needed by mwc_ssm_fwd for these sizes. */
+/* Workspace bytes needed by mwc_ssm_fwd for these sizes (0 when the sequence is not split into
+ * segments; otherwise the segment carries). dim is limited to 2^24. */
 size_t mwc_ssm_fwd_workspace_size(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate);
 
 /*
