@@ -86,6 +86,22 @@ int mwc_ssm_fwd(int dtype, const void* u, const void* delta, const void* A, cons
                 float* ckpt, int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate,
                 void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * mwc_ssm_fwd with the elementwise transforms a Mamba block applies around the scan, fused into
+ * the scan's loads and stores (no reference counterpart: the reference rejects them; they are the
+ * delta_bias / delta_softplus / z options of the official Mamba selective scan):
+ *   delta' = softplus(delta + delta_bias)   (delta_bias (dim,) may be NULL; delta_softplus 0/1)
+ *   out    = the scan of delta' (as mwc_ssm_fwd)          may be NULL
+ *   out_z  = out * silu(z)                  (z (batch, seqlen, dim) may be NULL; then out_z NULL;
+ *                                            out_z may be NULL with z, e.g. to rebuild checkpoints)
+ * Checkpoints, workspace and the other arguments are as for mwc_ssm_fwd.
+ */
+int mwc_ssm_fwd_ex(int dtype, const void* u, const void* delta, const void* A, const void* B_ssm,
+                   const void* C_ssm, const void* D_ssm, const void* h_prev, const void* delta_bias,
+                   int delta_softplus, const void* z, void* out, void* out_z, void* h_last, float* ckpt,
+                   int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
 /* Workspace bytes needed by mwc_ssm_bwd for these sizes. */
 size_t mwc_ssm_bwd_workspace_size(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate);
 
@@ -108,6 +124,20 @@ int mwc_ssm_bwd(int dtype, const void* u, const void* delta, const void* A, cons
                 int64_t dstate, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Workspace bytes needed by mwc_pscan_fwd / mwc_pscan_bwd for these sizes. */
+/*
+ * The adjoint of mwc_ssm_fwd_ex (no reference counterpart, see there). With z, `out` is the ungated
+ * forward output (mwc_ssm_fwd_ex's `out`) and dout the gradient of out_z; dz receives
+ * dout * out * silu'(z). ddelta is the gradient of the raw delta (through the bias and softplus),
+ * ddelta_bias (dim,) the gradient of delta_bias (may be NULL). Checkpoints (from mwc_ssm_fwd_ex with
+ * the same transforms), workspace and the other arguments are as for mwc_ssm_bwd.
+ */
+int mwc_ssm_bwd_ex(int dtype, const void* u, const void* delta, const void* A, const void* B_ssm,
+                   const void* C_ssm, const void* D_ssm, const void* h_prev, const void* delta_bias,
+                   int delta_softplus, const void* z, const void* out, const void* dout, const void* dh_last,
+                   const float* ckpt, void* du, void* ddelta, void* dA, void* dB, void* dC, void* dD,
+                   void* ddelta_bias, void* dz, void* dh_prev, int64_t batch, int64_t seqlen, int64_t dim,
+                   int64_t dstate, void* workspace, size_t workspace_bytes, void* stream);
+
 size_t mwc_pscan_workspace_size(int64_t nseq, int64_t seqlen, int64_t ncols);
 
 /*

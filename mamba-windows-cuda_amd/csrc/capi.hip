@@ -173,6 +173,7 @@ size_t bwd_workspace_bytes(const SsmShape& s) {
     size_t n = align256((size_t)bwd_groups(s, p.spl) * s.batch * s.seqlen * 32 * sizeof(float));  // dB/dC
     n += align256((size_t)p.nseg * s.batch * s.dim * kNState * sizeof(float));                      // dA
     n += align256((size_t)p.nseg * s.batch * s.dim * sizeof(float));                                // dD
+    n += align256((size_t)p.nseg * s.batch * s.dim * sizeof(float));                                // d bias
     n += 2 * carry_bytes(s, p);
     return n;
 }
@@ -210,16 +211,19 @@ size_t mwc_ssm_bwd_workspace_size(int64_t batch, int64_t seqlen, int64_t dim, in
     return mwc::bwd_workspace_bytes({batch, seqlen, dim});
 }
 
-int mwc_ssm_fwd(int dtype, const void* u, const void* delta, const void* A, const void* B_ssm, const void* C_ssm,
-                const void* D_ssm, const void* h_prev, void* out, void* h_last, float* ckpt, int64_t batch,
-                int64_t seqlen, int64_t dim, int64_t dstate, void* workspace, size_t workspace_bytes,
-                void* stream) {
+int mwc_ssm_fwd_ex(int dtype, const void* u, const void* delta, const void* A, const void* B_ssm,
+                   const void* C_ssm, const void* D_ssm, const void* h_prev, const void* delta_bias,
+                   int delta_softplus, const void* z, void* out, void* out_z, void* h_last, float* ckpt,
+                   int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate, void* workspace,
+                   size_t workspace_bytes, void* stream) {
     g_err[0] = 0;
     if (int st = check_dims(dtype, batch, seqlen, dim, dstate)) return st;
     if (batch == 0 || dim == 0) return MWC_OK;
     if (!A || !D_ssm) return fail(MWC_ERR_INVALID_ARGUMENT, "A and D_ssm must not be NULL");
     if (seqlen > 0 && (!u || !delta || !B_ssm || !C_ssm))
         return fail(MWC_ERR_INVALID_ARGUMENT, "u, delta, B_ssm and C_ssm must not be NULL");
+    if (z == nullptr && out_z != nullptr) return fail(MWC_ERR_INVALID_ARGUMENT, "out_z needs z");
+    const bool xf = delta_bias != nullptr || delta_softplus != 0 || z != nullptr;
     const mwc::SsmShape s{batch, seqlen, dim};
     const bool half = dtype == MWC_DTYPE_F16;
     hipStream_t st = (hipStream_t)stream;
@@ -227,6 +231,7 @@ int mwc_ssm_fwd(int dtype, const void* u, const void* delta, const void* A, cons
     if (seqlen > 0 && need > 0 && (workspace == nullptr || workspace_bytes < need))
         return fail(MWC_ERR_WORKSPACE, "forward workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
     if (mwc::impl_choice() == 3) {
+        if (xf) return fail(MWC_ERR_UNSUPPORTED, "delta_bias, delta_softplus and z need the default kernels");
         float* bcp = (float*)workspace;
         if (seqlen > 0) MWC_HIP_TRY(mwc::launch_v3_pack(half, B_ssm, C_ssm, bcp, s, st));
         MWC_HIP_TRY(mwc::launch_v3_fwd(half, u, delta, A, bcp, D_ssm, h_prev, out, h_last, ckpt, s, st));
@@ -236,16 +241,25 @@ int mwc_ssm_fwd(int dtype, const void* u, const void* delta, const void* A, cons
     float* car_h = (float*)workspace;
     float* car_x = (float*)((char*)workspace + need / 2);
     const mwc::FwdArgs a{u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, out, h_last, ckpt, car_h, car_x,
-                         p.nseg, p.cps, p.cfold, p.ncar};
+                         p.nseg, p.cps, p.cfold, p.ncar, mwc::ScanXf{delta_bias, z, delta_softplus != 0}, out_z};
     MWC_HIP_TRY(mwc::launch_ssm_fwd(half, p.spl, a, s, st));
     return MWC_OK;
 }
 
-int mwc_ssm_bwd(int dtype, const void* u, const void* delta, const void* A, const void* B_ssm, const void* C_ssm,
-                const void* D_ssm, const void* h_prev, const void* dout, const void* dh_last, const float* ckpt,
-                void* du, void* ddelta, void* dA, void* dB, void* dC, void* dD, void* dh_prev, int64_t batch,
+int mwc_ssm_fwd(int dtype, const void* u, const void* delta, const void* A, const void* B_ssm, const void* C_ssm,
+                const void* D_ssm, const void* h_prev, void* out, void* h_last, float* ckpt, int64_t batch,
                 int64_t seqlen, int64_t dim, int64_t dstate, void* workspace, size_t workspace_bytes,
                 void* stream) {
+    return mwc_ssm_fwd_ex(dtype, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, nullptr, 0, nullptr, out, nullptr,
+                          h_last, ckpt, batch, seqlen, dim, dstate, workspace, workspace_bytes, stream);
+}
+
+int mwc_ssm_bwd_ex(int dtype, const void* u, const void* delta, const void* A, const void* B_ssm,
+                   const void* C_ssm, const void* D_ssm, const void* h_prev, const void* delta_bias,
+                   int delta_softplus, const void* z, const void* out, const void* dout, const void* dh_last,
+                   const float* ckpt, void* du, void* ddelta, void* dA, void* dB, void* dC, void* dD,
+                   void* ddelta_bias, void* dz, void* dh_prev, int64_t batch, int64_t seqlen, int64_t dim,
+                   int64_t dstate, void* workspace, size_t workspace_bytes, void* stream) {
     g_err[0] = 0;
     (void)h_prev;  // the checkpoints already carry h_prev (checkpoint 0)
     if (int st = check_dims(dtype, batch, seqlen, dim, dstate)) return st;
@@ -254,6 +268,11 @@ int mwc_ssm_bwd(int dtype, const void* u, const void* delta, const void* A, cons
     if (seqlen > 0 && (!u || !delta || !B_ssm || !C_ssm || !dout || !ckpt || !du || !ddelta || !dB || !dC))
         return fail(MWC_ERR_INVALID_ARGUMENT,
                     "u, delta, B_ssm, C_ssm, dout, ckpt, du, ddelta, dB and dC must not be NULL");
+    if (seqlen > 0 && z != nullptr && (out == nullptr || dz == nullptr))
+        return fail(MWC_ERR_INVALID_ARGUMENT, "out (ungated) and dz must not be NULL when z is given");
+    if (ddelta_bias != nullptr && delta_bias == nullptr)
+        return fail(MWC_ERR_INVALID_ARGUMENT, "ddelta_bias needs delta_bias");
+    const bool xf = delta_bias != nullptr || delta_softplus != 0 || z != nullptr;
     const mwc::SsmShape s{batch, seqlen, dim};
     const size_t need = mwc::bwd_workspace_bytes(s);
     if (workspace == nullptr || workspace_bytes < need)
@@ -262,6 +281,7 @@ int mwc_ssm_bwd(int dtype, const void* u, const void* delta, const void* A, cons
     hipStream_t st = (hipStream_t)stream;
     char* w = (char*)workspace;
     if (mwc::impl_choice() == 3) {
+        if (xf) return fail(MWC_ERR_UNSUPPORTED, "delta_bias, delta_softplus and z need the default kernels");
         const int ngrp = mwc::v3_groups(s);
         float* bcp = (float*)w;
         w += mwc::v3_bcp_bytes(s);
@@ -273,7 +293,8 @@ int mwc_ssm_bwd(int dtype, const void* u, const void* delta, const void* A, cons
         if (seqlen > 0) MWC_HIP_TRY(mwc::launch_v3_pack(half, B_ssm, C_ssm, bcp, s, st));
         MWC_HIP_TRY(mwc::launch_v3_bwd(half, u, delta, A, bcp, D_ssm, dout, dh_last, ckpt, du, ddelta, dh_prev,
                                        dA_part, dD_part, dbc_part, s, st));
-        MWC_HIP_TRY(mwc::launch_bwd_finish(half, dbc_part, dA_part, dD_part, dB, dC, dA, dD, ngrp, (int)batch, s, st));
+        MWC_HIP_TRY(mwc::launch_bwd_finish(half, dbc_part, dA_part, dD_part, nullptr, dB, dC, dA, dD, nullptr, ngrp,
+                                           (int)batch, s, st));
         return MWC_OK;
     }
     const mwc::SegPlan p = mwc::plan_bwd(s);
@@ -284,15 +305,29 @@ int mwc_ssm_bwd(int dtype, const void* u, const void* delta, const void* A, cons
     w += align256((size_t)p.nseg * batch * dim * mwc::kNState * sizeof(float));
     float* dD_part = (float*)w;
     w += align256((size_t)p.nseg * batch * dim * sizeof(float));
+    float* dbias_part = (float*)w;
+    w += align256((size_t)p.nseg * batch * dim * sizeof(float));
     float* car_g = (float*)w;
     w += mwc::carry_bytes(s, p);
     float* car_x = (float*)w;
     const mwc::BwdArgs a{u, delta, A, B_ssm, C_ssm, D_ssm, dout, dh_last, ckpt, du, ddelta, dh_prev,
-                         dA_part, dD_part, dbc_part, car_g, car_x, p.nseg, p.cps, p.cfold, p.ncar};
+                         dA_part, dD_part, dbc_part, car_g, car_x, p.nseg, p.cps, p.cfold, p.ncar,
+                         mwc::ScanXf{delta_bias, z, delta_softplus != 0}, out, dz, dbias_part};
     MWC_HIP_TRY(mwc::launch_ssm_bwd(half, p.spl, a, s, st));
-    MWC_HIP_TRY(mwc::launch_bwd_finish(half, dbc_part, dA_part, dD_part, dB, dC, dA, dD, ngrp, p.nseg * (int)batch,
-                                       s, st));
+    MWC_HIP_TRY(mwc::launch_bwd_finish(half, dbc_part, dA_part, dD_part, dbias_part, dB, dC, dA, dD,
+                                       delta_bias != nullptr ? ddelta_bias : nullptr, ngrp, p.nseg * (int)batch, s,
+                                       st));
     return MWC_OK;
+}
+
+int mwc_ssm_bwd(int dtype, const void* u, const void* delta, const void* A, const void* B_ssm, const void* C_ssm,
+                const void* D_ssm, const void* h_prev, const void* dout, const void* dh_last, const float* ckpt,
+                void* du, void* ddelta, void* dA, void* dB, void* dC, void* dD, void* dh_prev, int64_t batch,
+                int64_t seqlen, int64_t dim, int64_t dstate, void* workspace, size_t workspace_bytes,
+                void* stream) {
+    return mwc_ssm_bwd_ex(dtype, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, nullptr, 0, nullptr, nullptr, dout, dh_last,
+                          ckpt, du, ddelta, dA, dB, dC, dD, nullptr, nullptr, dh_prev, batch, seqlen, dim, dstate,
+                          workspace, workspace_bytes, stream);
 }
 
 size_t mwc_pscan_workspace_size(int64_t nseq, int64_t seqlen, int64_t ncols) {

@@ -55,6 +55,10 @@ template <> __device__ __forceinline__ void buf_st<half_t>(rsrc_t r, uint32_t of
     __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, static_cast<half_t>(v)), r, off, 0, 0);
 }
 
+// Elementwise transforms around the scan (OCML expf/log1pf; fp32).
+__device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + expf(-x)); }
+
 // DPP lane exchanges within 16-lane rows (gfx9 DPP controls).
 template <int CTRL> __device__ __forceinline__ float dpp(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));

@@ -27,12 +27,23 @@ size_t fwd_workspace_bytes(const SsmShape& s);
 size_t bwd_workspace_bytes(const SsmShape& s);
 int bwd_groups(const SsmShape& s, int spl);  // channel groups that write dB/dC partials
 
+// Optional elementwise transforms fused around the scan (all NULL / 0: the plain scan).
+//   delta' = softplus(delta + delta_bias) (bias and softplus each optional; rows past L stay 0)
+//   out_z  = out * silu(z)
+struct ScanXf {
+    const void* delta_bias;  // (dim,)
+    const void* z;           // (batch, seqlen, dim)
+    int softplus;
+};
+
 struct FwdArgs {
     const void *u, *delta, *A, *B, *C, *Dv, *h_prev;
     void *out, *h_last;        // out == NULL: state-only pass (checkpoints and/or h_last)
     float* ckpt;               // [batch][nck][dim][16] or NULL
     float *car_h, *car_x;      // [batch][ncar][dim][16] carries (nseg > 1)
     int nseg, cps, cfold, ncar;
+    ScanXf xf;
+    void* out_z;               // gated output (xf.z != NULL); `out` then receives the ungated one
 };
 
 struct BwdArgs {
@@ -44,15 +55,20 @@ struct BwdArgs {
     float* dbc_part;           // [groups][batch][seqlen][32]
     float *car_g, *car_x;      // [batch][ncar][dim][16] adjoint carries (nseg > 1)
     int nseg, cps, cfold, ncar;
+    ScanXf xf;
+    const void* y;             // ungated forward output (xf.z != NULL)
+    void* dz;                  // gradient of z (xf.z != NULL)
+    float* dbias_part;         // [nseg][batch][dim] delta_bias partials (xf.delta_bias != NULL)
 };
 
 // Kernel launchers; `is_half` selects fp16 storage. They only enqueue work.
 hipError_t launch_ssm_fwd(bool is_half, int spl, const FwdArgs& a, const SsmShape& s, hipStream_t st);
 hipError_t launch_ssm_bwd(bool is_half, int spl, const BwdArgs& a, const SsmShape& s, hipStream_t st);
-// Sums the dB/dC partials of `ngroups` channel groups and the dA/dD partials of `nrows` rows.
+// Sums the dB/dC partials of `ngroups` channel groups and the dA/dD (and, when dbias is not NULL,
+// delta_bias) partials of `nrows` rows.
 hipError_t launch_bwd_finish(bool is_half, const float* dbc_part, const float* dA_part,
-                             const float* dD_part, void* dB, void* dC, void* dA, void* dD,
-                             int ngroups, int nrows, const SsmShape& s, hipStream_t st);
+                             const float* dD_part, const float* dbias_part, void* dB, void* dC, void* dA,
+                             void* dD, void* dbias, int ngroups, int nrows, const SsmShape& s, hipStream_t st);
 
 // "state groups across waves" kernels (ssm_v3.hip)
 int impl_choice();  // 2 = lane groups (default), 3 = state groups across waves

@@ -94,11 +94,11 @@ __device__ __forceinline__ void wave_lds_fence() {
 // car_g = the reverse sweep of g -> dA_t * (g + dout_t * C_t) over the carry
 // segment from g = 0, car_x = its summed base-2 decay exponents (so it maps an
 // adjoint g arriving from its right to 2^car_x * g + car_g).
-template <typename T, int SPL>
+template <typename T, int SPL, bool XF>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fwd_min_waves(SPL), 8)))
 ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const T* __restrict__ Cm,
                      const T* __restrict__ dout, float* __restrict__ car_g, float* __restrict__ car_x, int Bsz,
-                     int L, int D, int nck, int nblk_d, int ncar, int first, int cps) {
+                     int L, int D, int nck, int nblk_d, int ncar, int first, int cps, ScanXf xf) {
     constexpr int LPC = kNState / SPL;
     constexpr int CPW = 64 / LPC;
     constexpr int CPB = CPW * 4;
@@ -144,7 +144,10 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
     // buffer resources per chunk: rows past L and channels past D read as 0 (see the main kernel)
     const uint32_t lofs = lvalid ? ((uint32_t)(sg * SPG) * (uint32_t)D + (uint32_t)ld_d) * sizeof(T) : kOob;
     const uint32_t row_bytes = (uint32_t)D * sizeof(T);
-    T pd[SPG], py[SPG], pc;
+    const T* zb = XF && xf.z ? static_cast<const T*>(xf.z) : nullptr;
+    const bool xform = XF && (xf.delta_bias != nullptr || xf.softplus);
+    const float lbias = XF && xf.delta_bias ? ld(static_cast<const T*>(xf.delta_bias) + ld_d) : 0.f;
+    T pd[SPG], py[SPG], pz[SPG], pc;
     auto issue = [&](int k) {
         const int64_t ck = (int64_t)k * TC;
         const uint32_t rows = (uint32_t)min(TC, L - k * TC);
@@ -155,14 +158,30 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
             pd[s] = buf_raw<T>(rd, lofs + s * row_bytes);
             py[s] = buf_raw<T>(ry, lofs + s * row_bytes);
         }
+        if (XF && zb != nullptr) {
+            const rsrc_t rz = make_rsrc(zb + (row0 + ck) * D, rows * row_bytes);
+#pragma unroll
+            for (int s = 0; s < SPG; ++s) pz[s] = buf_raw<T>(rz, lofs + s * row_bytes);
+        }
         pc = buf_raw<T>(make_rsrc(Cm + (row0 + ck) * kNState, rows * kNState * sizeof(T)), tid * sizeof(T));
     };
-    auto commit = [&](int buf) {
+    auto commit = [&](int k, int buf) {
         float vd[SPG], vy[SPG];
 #pragma unroll
         for (int s = 0; s < SPG; ++s) {
             vd[s] = static_cast<float>(pd[s]);
             vy[s] = static_cast<float>(py[s]);
+            if constexpr (XF) {
+                if (xform) {
+                    vd[s] += lbias;
+                    if (xf.softplus) vd[s] = softplus_f(vd[s]);
+                    if (k * TC + sg * SPG + s >= L) vd[s] = 0.f;
+                }
+                if (zb != nullptr) {  // the scan sees dout * silu(z)
+                    const float zv = static_cast<float>(pz[s]);
+                    vy[s] *= zv * sigmoid_f(zv);
+                }
+            }
         }
         stv<SPG>(&s_in[buf][0][lc][sg * SPG], vd);
         stv<SPG>(&s_in[buf][1][lc][sg * SPG], vy);
@@ -171,7 +190,7 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
 
     if (k0 < k1) {
         issue(k1 - 1);
-        commit((k1 - 1) & 1);
+        commit(k1 - 1, (k1 - 1) & 1);
     }
     __syncthreads();
     for (int k = k1 - 1; k >= k0; --k) {
@@ -212,7 +231,7 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
 #pragma unroll
             for (int j = 0; j < SPL; ++j) xs[j] = __builtin_fmaf(A2[j], sdt, xs[j]);
         }
-        if (more) commit(buf ^ 1);
+        if (more) commit(k - 1, buf ^ 1);
         __syncthreads();
     }
     if (valid) {
@@ -222,7 +241,9 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
     }
 }
 
-template <typename T, int SPL>
+// XF: the elementwise transforms of ScanXf are compiled in (the plain scan does not carry their
+// registers).
+template <typename T, int SPL, bool XF>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_min_waves(SPL), 8)))
 ssm_bwd_kernel(
     const T* __restrict__ u, const T* __restrict__ delta, const T* __restrict__ A, const T* __restrict__ Bm,
@@ -230,7 +251,8 @@ ssm_bwd_kernel(
     const float* __restrict__ ckpt, T* __restrict__ du, T* __restrict__ ddelta, T* __restrict__ dh_prev,
     float* __restrict__ dA_part, float* __restrict__ dD_part, float* __restrict__ dbc_part,
     const float* __restrict__ car_g, const float* __restrict__ car_x, int Bsz, int L, int D, int nck, int nblk_d,
-    int nseg, int cps, int ncar, int cfold) {
+    int nseg, int cps, int ncar, int cfold, ScanXf xf, const T* __restrict__ yb_out, T* __restrict__ dz,
+    float* __restrict__ dbias_part) {
     constexpr int LPC = kNState / SPL;
     constexpr int CPW = 64 / LPC;
     constexpr int CPB = CPW * 4;
@@ -309,7 +331,9 @@ ssm_bwd_kernel(
     const uint32_t row_bytes = (uint32_t)D * sizeof(T);
     auto chunk_rows = [&](int k) { return (uint32_t)min(TC, L - k * TC); };
     const int64_t rowD = row0 * D;
-    T pu[SPG], pd[SPG], py[SPG], pb, pc;
+    const T* zb = XF && xf.z ? static_cast<const T*>(xf.z) : nullptr;
+    const bool xform = XF && (xf.delta_bias != nullptr || xf.softplus);
+    T pu[SPG], pd[SPG], py[SPG], pz[SPG], pyo[SPG], pb, pc;
     float hnext[SPL];
     auto issue = [&](int k) {
         const int64_t ck = (int64_t)k * TC;
@@ -323,6 +347,15 @@ ssm_bwd_kernel(
             pd[s] = buf_raw<T>(rd, lofs + s * row_bytes);
             py[s] = buf_raw<T>(ry, lofs + s * row_bytes);
         }
+        if (XF && zb != nullptr) {  // z and the ungated output, for dout * silu(z) and dz
+            const rsrc_t rz = make_rsrc(zb + rowD + ck * D, rows * row_bytes);
+            const rsrc_t ro = make_rsrc(yb_out + rowD + ck * D, rows * row_bytes);
+#pragma unroll
+            for (int s = 0; s < SPG; ++s) {
+                pz[s] = buf_raw<T>(rz, lofs + s * row_bytes);
+                pyo[s] = buf_raw<T>(ro, lofs + s * row_bytes);
+            }
+        }
         const uint32_t bc_bytes = rows * kNState * sizeof(T);
         pb = buf_raw<T>(make_rsrc(Bm + (row0 + ck) * kNState, bc_bytes), tid * sizeof(T));
         pc = buf_raw<T>(make_rsrc(Cm + (row0 + ck) * kNState, bc_bytes), tid * sizeof(T));
@@ -332,16 +365,45 @@ ssm_bwd_kernel(
 #pragma unroll
     for (int n = 0; n < kNState; ++n) lamax2 = __builtin_fmaxf(lamax2, __builtin_fabsf(ld(A + (int64_t)ld_d * kNState + n)));
     lamax2 *= kLog2e;
+    const float lbias = XF && xf.delta_bias ? ld(static_cast<const T*>(xf.delta_bias) + ld_d) : 0.f;
+    // d delta / d delta' (softplus) of the loader's elements, for the chunk being stored and the next
+    float dd_cur[XF ? SPG : 1], dd_nxt[XF ? SPG : 1];
+    float dbias_acc = 0.f;
     auto commit = [&](int k) {
         float vd[SPG], vdu[SPG], vu[SPG], vy[SPG];
         float vmax = 0.f;
+        [[maybe_unused]] float vdz[SPG];
 #pragma unroll
         for (int s = 0; s < SPG; ++s) {
             vd[s] = static_cast<float>(pd[s]);
             vu[s] = static_cast<float>(pu[s]);
             vy[s] = static_cast<float>(py[s]);
+            if constexpr (XF) {
+                dd_nxt[s] = 1.f;
+                if (xform) {
+                    vd[s] += lbias;
+                    if (xf.softplus) {
+                        dd_nxt[s] = sigmoid_f(vd[s]);
+                        vd[s] = softplus_f(vd[s]);
+                    }
+                    if (k * TC + sg * SPG + s >= L) vd[s] = 0.f;
+                }
+                if (zb != nullptr) {  // out_z = out * silu(z): the scan sees dout * silu(z)
+                    const float zv = static_cast<float>(pz[s]);
+                    const float sz = sigmoid_f(zv);
+                    vdz[s] = vy[s] * static_cast<float>(pyo[s]) * sz * (1.f + zv * (1.f - sz));
+                    vy[s] *= zv * sz;
+                }
+            }
             vdu[s] = vd[s] * vu[s];
             vmax = __builtin_fmaxf(vmax, __builtin_fabsf(vd[s]));
+        }
+        if constexpr (XF) {
+            if (zb != nullptr) {  // dz = dout * out * silu'(z) needs no scan: store it now
+                const rsrc_t rdz = make_rsrc(dz + rowD + (int64_t)k * TC * D, chunk_rows(k) * row_bytes);
+#pragma unroll
+                for (int s = 0; s < SPG; ++s) buf_st<T>(rdz, lofs + s * row_bytes, vdz[s]);
+            }
         }
         if (vmax * lamax2 > kExp2Clamp) s_flag = k;  // benign race: every writer stores k
         stv<SPG>((s_in(0, lc) + sg * SPG), vd);
@@ -369,6 +431,10 @@ ssm_bwd_kernel(
     for (int k = k1 - 1; k >= k0; --k) {
         const int t0 = k * TC;
         const bool more = k > k0;
+        if constexpr (XF) {
+#pragma unroll
+            for (int s = 0; s < SPG; ++s) dd_cur[s] = dd_nxt[s];
+        }
         if (more) issue(k - 1);
         // one workgroup-uniform decision per chunk: the clamped path gives the same values whenever
         // no exponent reaches the clamp, so deciding for the whole workgroup is exact
@@ -508,7 +574,12 @@ ssm_bwd_kernel(
 #pragma unroll
             for (int s = 0; s < SPG; ++s) {
                 buf_st<T>(rdu, lofs + s * row_bytes, s_out[0][sg * SPG + s][lc]);
-                buf_st<T>(rdd, lofs + s * row_bytes, s_out[1][sg * SPG + s][lc]);
+                float dd = s_out[1][sg * SPG + s][lc];
+                if constexpr (XF) {
+                    dd *= dd_cur[s];  // through softplus (1 without it)
+                    if (t0 + sg * SPG + s < L) dbias_acc += dd;
+                }
+                buf_st<T>(rdd, lofs + s * row_bytes, dd);
             }
         }
         // this workgroup's dB/dC partial for the chunk (sum of its 4 waves)
@@ -529,6 +600,19 @@ ssm_bwd_kernel(
         stv<SPL>(dA_part + (pr * D + d) * kNState + n0, dAacc);
         if (g == 0) dD_part[pr * D + d] = dDacc;
     }
+    if constexpr (XF) {
+        if (xf.delta_bias != nullptr) {  // delta_bias partial: the NSG loader threads of a channel, in order
+            __syncthreads();
+            float* red = &s_out[0][0][0];  // free after the chunk loop; NSG*CPB <= 2*TC*OS floats
+            red[sg * CPB + lc] = dbias_acc;
+            __syncthreads();
+            if (tid < CPB && d0 + tid < D) {
+                float acc = 0.f;
+                for (int q = 0; q < NSG; ++q) acc += red[q * CPB + tid];
+                dbias_part[((int64_t)seg * Bsz + b) * D + d0 + tid] = acc;
+            }
+        }
+    }
 }
 
 // The backward's reductions, one launch: blocks [0, nblk_bc) sum the channel-group dB/dC partials
@@ -539,7 +623,8 @@ __global__ void __launch_bounds__(256) bwd_finish_kernel(const float* __restrict
                                                          T* __restrict__ dC, int ngrp, int64_t rows, int nblk_bc,
                                                          const float* __restrict__ dA_part,
                                                          const float* __restrict__ dD_part, T* __restrict__ dA,
-                                                         T* __restrict__ dD, int nrows, int D) {
+                                                         T* __restrict__ dD, int nrows, int D,
+                                                         const float* __restrict__ dbias_part, T* __restrict__ dbias) {
     if ((int)blockIdx.x < nblk_bc) {
         const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;  // over rows*32, 4-aligned
         if (i >= rows * 32) return;
@@ -584,6 +669,11 @@ __global__ void __launch_bounds__(256) bwd_finish_kernel(const float* __restrict
         float s = 0.f;
         for (int r = 0; r < nrows; ++r) s += dD_part[(int64_t)r * D + dd];
         st(dD + dd, s);
+    } else if (dbias != nullptr && i < nA + 2 * D) {
+        const int64_t dd = i - nA - D;
+        float s = 0.f;
+        for (int r = 0; r < nrows; ++r) s += dbias_part[(int64_t)r * D + dd];
+        st(dbias + dd, s);
     }
 }
 
@@ -592,21 +682,28 @@ int bwd_groups(const SsmShape& s, int spl) {
     return (int)((s.dim + cpb - 1) / cpb);
 }
 
-template <typename T, int SPL>
+template <typename T, int SPL, bool XF>
 static hipError_t bwd_inst(const BwdArgs& a, const SsmShape& s, hipStream_t st) {
     const int nblk_d = bwd_groups(s, SPL);
     const int nck = (int)((s.seqlen + kCkptSteps - 1) / kCkptSteps);
     const int per_seg = nblk_d * (int)s.batch;
     if (a.nseg > 1)  // carries of every chunk after the first segment
-        hipLaunchKernelGGL((ssm_bwd_carry_kernel<T, SPL>), dim3(per_seg * a.ncar), dim3(256), 0, st,
+        hipLaunchKernelGGL((ssm_bwd_carry_kernel<T, SPL, XF>), dim3(per_seg * a.ncar), dim3(256), 0, st,
                            (const T*)a.delta, (const T*)a.A, (const T*)a.C, (const T*)a.dout, a.car_g, a.car_x,
-                           (int)s.batch, (int)s.seqlen, (int)s.dim, nck, nblk_d, a.ncar, a.cps, a.cps / a.cfold);
-    hipLaunchKernelGGL((ssm_bwd_kernel<T, SPL>), dim3(per_seg * a.nseg), dim3(256), 0, st, (const T*)a.u,
+                           (int)s.batch, (int)s.seqlen, (int)s.dim, nck, nblk_d, a.ncar, a.cps, a.cps / a.cfold,
+                           a.xf);
+    hipLaunchKernelGGL((ssm_bwd_kernel<T, SPL, XF>), dim3(per_seg * a.nseg), dim3(256), 0, st, (const T*)a.u,
                        (const T*)a.delta, (const T*)a.A, (const T*)a.B, (const T*)a.C, (const T*)a.Dv,
                        (const T*)a.dout, (const T*)a.dh_last, a.ckpt, (T*)a.du, (T*)a.ddelta, (T*)a.dh_prev,
                        a.dA_part, a.dD_part, a.dbc_part, a.car_g, a.car_x, (int)s.batch, (int)s.seqlen, (int)s.dim,
-                       nck, nblk_d, a.nseg, a.cps, a.ncar, a.cfold);
+                       nck, nblk_d, a.nseg, a.cps, a.ncar, a.cfold, a.xf, (const T*)a.y, (T*)a.dz, a.dbias_part);
     return hipGetLastError();
+}
+
+template <typename T, int SPL>
+static hipError_t bwd_inst(const BwdArgs& a, const SsmShape& s, hipStream_t st) {
+    const bool xf = a.xf.delta_bias != nullptr || a.xf.softplus || a.xf.z != nullptr;
+    return xf ? bwd_inst<T, SPL, true>(a, s, st) : bwd_inst<T, SPL, false>(a, s, st);
 }
 
 hipError_t launch_ssm_bwd(bool is_half, int spl, const BwdArgs& a, const SsmShape& s, hipStream_t st) {
@@ -620,22 +717,26 @@ hipError_t launch_ssm_bwd(bool is_half, int spl, const BwdArgs& a, const SsmShap
 }
 
 template <typename T>
-static hipError_t finish_t(const float* dbc_part, const float* dA_part, const float* dD_part, void* dB, void* dC,
-                           void* dA, void* dD, int ngrp, int nrows, const SsmShape& s, hipStream_t st) {
+static hipError_t finish_t(const float* dbc_part, const float* dA_part, const float* dD_part,
+                           const float* dbias_part, void* dB, void* dC, void* dA, void* dD, void* dbias, int ngrp,
+                           int nrows, const SsmShape& s, hipStream_t st) {
     const int64_t rows = s.batch * s.seqlen;
     const int nblk_bc = (int)((rows * 32 / 4 + 255) / 256);
-    const int64_t n2 = s.dim * kNState + s.dim;
+    const int64_t n2 = s.dim * kNState + 2 * s.dim;
     const int nblk_ad = (int)((n2 + 255) / 256);
     hipLaunchKernelGGL(bwd_finish_kernel<T>, dim3(nblk_bc + nblk_ad), dim3(256), 0, st, dbc_part, (T*)dB, (T*)dC,
-                       ngrp, rows, nblk_bc, dA_part, dD_part, (T*)dA, (T*)dD, nrows, (int)s.dim);
+                       ngrp, rows, nblk_bc, dA_part, dD_part, (T*)dA, (T*)dD, nrows, (int)s.dim, dbias_part,
+                       (T*)dbias);
     return hipGetLastError();
 }
 
 hipError_t launch_bwd_finish(bool is_half, const float* dbc_part, const float* dA_part, const float* dD_part,
-                             void* dB, void* dC, void* dA, void* dD, int ngroups, int nrows, const SsmShape& s,
-                             hipStream_t st) {
-    return is_half ? finish_t<half_t>(dbc_part, dA_part, dD_part, dB, dC, dA, dD, ngroups, nrows, s, st)
-                   : finish_t<float>(dbc_part, dA_part, dD_part, dB, dC, dA, dD, ngroups, nrows, s, st);
+                             const float* dbias_part, void* dB, void* dC, void* dA, void* dD, void* dbias,
+                             int ngroups, int nrows, const SsmShape& s, hipStream_t st) {
+    return is_half ? finish_t<half_t>(dbc_part, dA_part, dD_part, dbias_part, dB, dC, dA, dD, dbias, ngroups, nrows,
+                                      s, st)
+                   : finish_t<float>(dbc_part, dA_part, dD_part, dbias_part, dB, dC, dA, dD, dbias, ngroups, nrows,
+                                     s, st);
 }
 
 }  // namespace mwc

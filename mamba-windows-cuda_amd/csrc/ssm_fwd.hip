@@ -72,13 +72,15 @@ __device__ __forceinline__ void vst(float* p, const float (&v)[K]) {
 
 enum FwdMode { kMain = 0, kState = 1, kCarry = 2 };
 
-template <typename T, int SPL, int MODE>
+// XF: the elementwise transforms of ScanXf are compiled in (the plain scan does not carry their
+// registers).
+template <typename T, int SPL, int MODE, bool XF>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fwd_min_waves(SPL), 8)))
 ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __restrict__ A,
                const T* __restrict__ Bm, const T* __restrict__ Cm, const T* __restrict__ Dv,
                const T* __restrict__ h_prev, T* __restrict__ out, T* __restrict__ h_last, float* __restrict__ ckpt,
                float* __restrict__ car_h, float* __restrict__ car_x, int Bsz, int L, int D, int nck, int nblk_d,
-               int nseg, int cps, int ncar, int cfold) {
+               int nseg, int cps, int ncar, int cfold, ScanXf xf, T* __restrict__ out_z) {
     constexpr bool HAS_OUT = MODE == kMain;
     constexpr bool CARRY = MODE == kCarry;
     constexpr int LPC = kNState / SPL;  // lanes per channel
@@ -149,7 +151,9 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
     const uint32_t lofs = lvalid ? ((uint32_t)(sg * SPG) * (uint32_t)D + (uint32_t)ld_d) * sizeof(T) : kOob;
     const uint32_t row_bytes = (uint32_t)D * sizeof(T);
     auto chunk_rows = [&](int k) { return (uint32_t)min(TC, L - k * TC); };
-    T pu[SPG], pd[SPG], pb, pc;
+    // z is read only when the gated output is stored
+    const T* zb = XF && HAS_OUT && xf.z && out_z ? static_cast<const T*>(xf.z) + row0 * D : nullptr;
+    T pu[SPG], pd[SPG], pz[SPG], pb, pc;
     auto issue = [&](int k) {
         const int64_t ck = (int64_t)k * TC;
         const uint32_t rows = chunk_rows(k);
@@ -160,21 +164,38 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
             pu[s] = buf_raw<T>(ru, lofs + s * row_bytes);
             pd[s] = buf_raw<T>(rd, lofs + s * row_bytes);
         }
+        if (XF && zb != nullptr) {
+            const rsrc_t rz = make_rsrc(zb + ck * D, rows * row_bytes);
+#pragma unroll
+            for (int s = 0; s < SPG; ++s) pz[s] = buf_raw<T>(rz, lofs + s * row_bytes);
+        }
         pb = buf_raw<T>(make_rsrc(Bb + ck * kNState, rows * kNState * sizeof(T)), tid * sizeof(T));
         if constexpr (HAS_OUT) pc = buf_raw<T>(make_rsrc(Cb + ck * kNState, rows * kNState * sizeof(T)), tid * sizeof(T));
     };
     // D*u of the loader's (channel, steps) for the chunk being computed and the next one; the
     // loader thread also stores those outputs, so the consumer lanes never touch u
     const float Dl = HAS_OUT ? ld(Dv + ld_d) : 0.f;
-    float du_cur[SPG], du_nxt[SPG];
-    auto commit = [&](int buf) {
+    // delta' = softplus(delta + bias): applied once per element here; rows past L stay 0
+    const bool xform = XF && (xf.delta_bias != nullptr || xf.softplus);
+    const float lbias = XF && xf.delta_bias ? ld(static_cast<const T*>(xf.delta_bias) + ld_d) : 0.f;
+    float du_cur[SPG], du_nxt[SPG], gz_cur[SPG], gz_nxt[SPG];
+    auto commit = [&](int k, int buf) {
         float vd[SPG], vdu[SPG];
 #pragma unroll
         for (int s = 0; s < SPG; ++s) {
             vd[s] = static_cast<float>(pd[s]);
+            if (XF && xform) {
+                vd[s] += lbias;
+                if (xf.softplus) vd[s] = softplus_f(vd[s]);
+                if (k * TC + sg * SPG + s >= L) vd[s] = 0.f;
+            }
             const float vu = static_cast<float>(pu[s]);
             vdu[s] = vd[s] * vu;
             du_nxt[s] = Dl * vu;
+            if (XF && zb != nullptr) {
+                const float zv = static_cast<float>(pz[s]);
+                gz_nxt[s] = zv * sigmoid_f(zv);  // silu(z)
+            }
         }
         vst<SPG>(&s_in[buf][0][lc][sg * SPG], vd);
         vst<SPG>(&s_in[buf][1][lc][sg * SPG], vdu);
@@ -184,17 +205,20 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
 
     if (k0 < k1) {  // every segment holds a chunk unless L == 0 (then h_last = h_prev)
         issue(k0);
-        commit(k0 & 1);
+        commit(k0, k0 & 1);
     }
     __syncthreads();
     float* ckb = (!CARRY && ckpt) ? ckpt + ((int64_t)b * nck * D + d) * kNState + n0 : nullptr;
-    T* ob = HAS_OUT ? out + row0 * D : nullptr;
+    T* ob = HAS_OUT && out != nullptr ? out + row0 * D : nullptr;
 
     for (int k = k0; k < k1; ++k) {
         const int buf = k & 1;
         const bool more = k + 1 < k1;
 #pragma unroll
-        for (int s = 0; s < SPG; ++s) du_cur[s] = du_nxt[s];
+        for (int s = 0; s < SPG; ++s) {
+            du_cur[s] = du_nxt[s];
+            if constexpr (XF) gz_cur[s] = gz_nxt[s];
+        }
         if (more) issue(k + 1);
         if (ckb != nullptr && valid) vst<SPL>(ckb + (int64_t)k * D * kNState, h);
 
@@ -245,13 +269,19 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
                 for (int j = 0; j < SPL; ++j) xs[j] = __builtin_fmaf(A2[j], sdt, xs[j]);
             }
         }
-        if (more) commit(buf ^ 1);
+        if (more) commit(k + 1, buf ^ 1);
         __syncthreads();
         if constexpr (HAS_OUT) {
             // the loader's (channel, steps) outputs: y from the tile plus D*u
-            const rsrc_t ro = make_rsrc(ob + (int64_t)k * TC * D, chunk_rows(k) * row_bytes);
+            const uint32_t obytes = chunk_rows(k) * row_bytes;
+            const rsrc_t ro = make_rsrc(ob + (int64_t)k * TC * D, ob != nullptr ? obytes : 0);
+            const rsrc_t rz = make_rsrc(out_z + row0 * D + (int64_t)k * TC * D, XF && zb != nullptr ? obytes : 0);
 #pragma unroll
-            for (int s = 0; s < SPG; ++s) buf_st<T>(ro, lofs + s * row_bytes, s_y[buf][sg * SPG + s][lc] + du_cur[s]);
+            for (int s = 0; s < SPG; ++s) {
+                const float y = s_y[buf][sg * SPG + s][lc] + du_cur[s];
+                buf_st<T>(ro, lofs + s * row_bytes, y);  // size 0 when out is not wanted: dropped
+                if (XF && zb != nullptr) buf_st<T>(rz, lofs + s * row_bytes, y * gz_cur[s]);
+            }
         }
     }
     if constexpr (CARRY) {
@@ -265,27 +295,33 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
     }
 }
 
-template <typename T, int SPL, int MODE>
+template <typename T, int SPL, int MODE, bool XF>
 static void fwd_launch(const FwdArgs& a, const SsmShape& s, int nseg_launched, hipStream_t st) {
     constexpr int CPB = 4 * 64 / (kNState / SPL);
     const int nblk_d = (int)((s.dim + CPB - 1) / CPB);
     const int nck = (int)((s.seqlen + kCkptSteps - 1) / kCkptSteps);
     const int grid = nblk_d * (int)s.batch * nseg_launched;
-    hipLaunchKernelGGL((ssm_fwd_kernel<T, SPL, MODE>), dim3(grid), dim3(256), 0, st, (const T*)a.u,
+    hipLaunchKernelGGL((ssm_fwd_kernel<T, SPL, MODE, XF>), dim3(grid), dim3(256), 0, st, (const T*)a.u,
                        (const T*)a.delta, (const T*)a.A, (const T*)a.B, (const T*)a.C, (const T*)a.Dv,
                        (const T*)a.h_prev, (T*)a.out, (T*)a.h_last, a.ckpt, a.car_h, a.car_x, (int)s.batch,
                        (int)s.seqlen, (int)s.dim, nck, nblk_d, a.nseg, MODE == kCarry ? a.cps / a.cfold : a.cps,
-                       a.ncar, a.cfold);
+                       a.ncar, a.cfold, a.xf, (T*)a.out_z);
+}
+
+template <typename T, int SPL, bool XF>
+static hipError_t fwd_inst(const FwdArgs& a, const SsmShape& s, hipStream_t st) {
+    if (a.nseg > 1) fwd_launch<T, SPL, kCarry, XF>(a, s, a.ncar, st);  // carries of all chunks before the last segment
+    if (a.out != nullptr || a.out_z != nullptr)
+        fwd_launch<T, SPL, kMain, XF>(a, s, a.nseg, st);
+    else
+        fwd_launch<T, SPL, kState, XF>(a, s, a.nseg, st);
+    return hipGetLastError();
 }
 
 template <typename T, int SPL>
 static hipError_t fwd_inst(const FwdArgs& a, const SsmShape& s, hipStream_t st) {
-    if (a.nseg > 1) fwd_launch<T, SPL, kCarry>(a, s, a.ncar, st);  // carries of all chunks before the last segment
-    if (a.out != nullptr)
-        fwd_launch<T, SPL, kMain>(a, s, a.nseg, st);
-    else
-        fwd_launch<T, SPL, kState>(a, s, a.nseg, st);
-    return hipGetLastError();
+    const bool xf = a.xf.delta_bias != nullptr || a.xf.softplus || a.xf.z != nullptr;
+    return xf ? fwd_inst<T, SPL, true>(a, s, st) : fwd_inst<T, SPL, false>(a, s, st);
 }
 
 hipError_t launch_ssm_fwd(bool is_half, int spl, const FwdArgs& a, const SsmShape& s, hipStream_t st) {

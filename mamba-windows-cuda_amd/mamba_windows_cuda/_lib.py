@@ -34,9 +34,16 @@ _SIGNATURES = {
     "mwc_ssm_ckpt_count": ([I64], I64),
     "mwc_ssm_fwd_workspace_size": ([I64, I64, I64, I64], SZ),
     "mwc_ssm_fwd": ([ctypes.c_int, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, P, SZ, P], ctypes.c_int),
+    # dtype, u, delta, A, B, C, D, h_prev, delta_bias, softplus, z, out, out_z, h_last, ckpt, sizes, ws
+    "mwc_ssm_fwd_ex": ([ctypes.c_int, P, P, P, P, P, P, P, P, ctypes.c_int, P, P, P, P, P, I64, I64, I64, I64,
+                        P, SZ, P], ctypes.c_int),
     "mwc_ssm_bwd_workspace_size": ([I64, I64, I64, I64], SZ),
     "mwc_ssm_bwd": ([ctypes.c_int, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, P, SZ, P],
                     ctypes.c_int),
+    # dtype, u, delta, A, B, C, D, h_prev, delta_bias, softplus, z, out, dout, dh_last, ckpt,
+    # du, ddelta, dA, dB, dC, dD, ddelta_bias, dz, dh_prev, sizes, ws
+    "mwc_ssm_bwd_ex": ([ctypes.c_int, P, P, P, P, P, P, P, P, ctypes.c_int, P, P, P, P, P, P, P, P, P, P, P, P, P,
+                        P, I64, I64, I64, I64, P, SZ, P], ctypes.c_int),
     "mwc_pscan_workspace_size": ([I64, I64, I64], SZ),
     "mwc_pscan_fwd": ([ctypes.c_int, P, P, P, I64, I64, I64, P, SZ, P], ctypes.c_int),
     "mwc_pscan_bwd": ([ctypes.c_int, P, P, P, P, P, I64, I64, I64, P, SZ, P], ctypes.c_int),

@@ -27,46 +27,56 @@ import torch
 from . import ops
 
 
-def _forward_impl(ctx, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, checkpoint_lvl):
+def _forward_impl(ctx, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, checkpoint_lvl, z=None, delta_bias=None,
+                  delta_softplus=False):
     if checkpoint_lvl not in (0, 1):
         raise RuntimeError(f"checkpoint_lvl must be 0 or 1 (got {checkpoint_lvl})")
-    n_in = 7 if h_prev is not None else 6
-    need_grad = any(ctx.needs_input_grad[:n_in])
-    out, h_last, ckpt = ops.ssm_forward(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev,
-                                        want_ckpt=need_grad and checkpoint_lvl == 0)
+    grads_of = list(ctx.needs_input_grad[:6]) + [h_prev is not None and ctx.needs_input_grad[6]]
+    if len(ctx.needs_input_grad) > 8:  # the transform arguments (z, delta_bias)
+        grads_of += [z is not None and ctx.needs_input_grad[8], delta_bias is not None and ctx.needs_input_grad[9]]
+    need_grad = any(grads_of)
+    out, out_ungated, h_last, ckpt = ops.ssm_forward_xf(
+        u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, delta_bias=delta_bias, delta_softplus=delta_softplus, z=z,
+        want_ungated=need_grad and z is not None, want_ckpt=need_grad and checkpoint_lvl == 0)
     ctx.has_h_prev = h_prev is not None
     ctx.need_grad = need_grad
+    ctx.delta_softplus = bool(delta_softplus)
     if need_grad:
-        ctx.save_for_backward(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, ckpt)
+        ctx.save_for_backward(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, ckpt, z, delta_bias, out_ungated)
     ctx.set_materialize_grads(False)
     return out, h_last
 
 
 def _backward_impl(ctx, dout, dh_last):
-    u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, ckpt = ctx.saved_tensors
-    if ckpt is None:  # recompute level: rebuild the state checkpoints
-        _, _, ckpt = ops.ssm_forward(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, want_out=False,
-                                     want_h_last=False, want_ckpt=True)
+    u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, ckpt, z, delta_bias, out_ungated = ctx.saved_tensors
+    xf = dict(delta_bias=delta_bias, delta_softplus=ctx.delta_softplus, z=z)
+    if ckpt is None:  # recompute level: rebuild the state checkpoints (and the ungated output for dz)
+        _, out_ungated, _, ckpt = ops.ssm_forward_xf(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, want_out=False,
+                                                     want_ungated=z is not None, want_h_last=False,
+                                                     want_ckpt=True, **xf)
     if dout is None:
         dout = torch.zeros_like(u)
     want_dh_prev = ctx.has_h_prev and ctx.needs_input_grad[6]
-    du, ddelta, dA, dB, dC, dD, dh_prev = ops.ssm_backward(u, delta, A, B_ssm, C_ssm, D_ssm, dout, ckpt,
-                                                           dh_last, want_dh_prev=want_dh_prev)
-    return du, ddelta, dA, dB, dC, dD, dh_prev
+    return ops.ssm_backward_xf(u, delta, A, B_ssm, C_ssm, D_ssm, dout, ckpt, dh_last, want_dh_prev=want_dh_prev,
+                               out_ungated=out_ungated, **xf)
 
 
 class SelectiveScanCudaFunction(torch.autograd.Function):
-    """(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None) -> (out, h_last);
-    backward returns dh_prev when h_prev is given (mamba_cuda.py:1044-1096)."""
+    """(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, checkpoint_lvl=0, z=None, delta_bias=None,
+    delta_softplus=False) -> (out, h_last); backward returns dh_prev when h_prev is given
+    (mamba_cuda.py:1044-1096). The last three arguments are the fused transforms (delta' =
+    softplus(delta + delta_bias), out = scan * silu(z)); the reference has no counterpart."""
 
     @staticmethod
-    def forward(ctx, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, checkpoint_lvl=0):
-        return _forward_impl(ctx, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, checkpoint_lvl)
+    def forward(ctx, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, checkpoint_lvl=0, z=None, delta_bias=None,
+                delta_softplus=False):
+        return _forward_impl(ctx, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, checkpoint_lvl, z, delta_bias,
+                             delta_softplus)
 
     @staticmethod
     def backward(ctx, dout, dh_last):
-        g = _backward_impl(ctx, dout, dh_last)
-        return (*g, None)
+        du, ddelta, dA, dB, dC, dD, dh_prev, dbias, dz = _backward_impl(ctx, dout, dh_last)
+        return du, ddelta, dA, dB, dC, dD, dh_prev, None, dz, dbias, None
 
 
 class SelectiveScanFn(torch.autograd.Function):
@@ -79,7 +89,7 @@ class SelectiveScanFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_out):
-        return _backward_impl(ctx, grad_out, None)[:6]
+        return tuple(_backward_impl(ctx, grad_out, None)[:6])
 
 
 class SelectiveScanFnV2(torch.autograd.Function):
@@ -92,7 +102,7 @@ class SelectiveScanFnV2(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_out):
-        return _backward_impl(ctx, grad_out, None)[:6]
+        return tuple(_backward_impl(ctx, grad_out, None)[:6])
 
 
 class SelectiveScanCuda(torch.nn.Module):
@@ -104,19 +114,29 @@ class SelectiveScanCuda(torch.nn.Module):
     All tensors fp32 or all fp16, on the GPU; outputs and gradients take the
     input dtype. ``checkpoint_lvl`` (keyword, default 0) picks the memory/speed
     trade-off described in the module docstring.
+
+    Keyword-only extras fused into the kernels (not in the reference; the
+    options a Mamba block applies around the scan): ``delta_bias`` (D,) and
+    ``delta_softplus`` give delta' = softplus(delta + delta_bias); ``z``
+    (B, L, D) gates the output, out * silu(z). Gradients flow to z and
+    delta_bias.
     """
 
     def __init__(self, checkpoint_lvl: int = 0):
         super().__init__()
         self.checkpoint_lvl = checkpoint_lvl
 
-    def forward(self, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None):
-        out, _ = SelectiveScanCudaFunction.apply(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, self.checkpoint_lvl)
+    def forward(self, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, *, z=None, delta_bias=None,
+                delta_softplus=False):
+        out, _ = SelectiveScanCudaFunction.apply(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, self.checkpoint_lvl, z,
+                                                 delta_bias, delta_softplus)
         return out
 
-    def forward_with_state(self, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None):
+    def forward_with_state(self, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, *, z=None, delta_bias=None,
+                           delta_softplus=False):
         """Returns (out (B, L, D), h_last (B, D, N)); h_last feeds the next chunk's h_prev."""
-        return SelectiveScanCudaFunction.apply(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, self.checkpoint_lvl)
+        return SelectiveScanCudaFunction.apply(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, self.checkpoint_lvl, z,
+                                               delta_bias, delta_softplus)
 
 
 def selective_scan_ref(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, return_intermediates=False):

@@ -76,34 +76,63 @@ def ckpt_count(seqlen: int) -> int:
     return int(_lib.lib().mwc_ssm_ckpt_count(seqlen))
 
 
-def ssm_forward(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, *, want_out=True, want_h_last=True,
-                want_ckpt=False):
-    """Fused forward. Returns (out or None, h_last or None, ckpt or None).
+def check_transforms(u, delta_bias=None, z=None):
+    """The optional elementwise transforms around the scan: delta_bias (D,), z (B, L, D)."""
+    bsz, L, dm = u.shape
+    for name, t, shape in (("delta_bias", delta_bias, (dm,)), ("z", z, (bsz, L, dm))):
+        if t is None:
+            continue
+        _require(t.device == u.device, f"{name} must be on the same device as u")
+        _require(t.dtype == u.dtype, f"{name} dtype must match u dtype")
+        _require(tuple(t.shape) == shape, f"{name} shape must be {shape}")
+
+
+def ssm_forward_xf(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, *, delta_bias=None, delta_softplus=False,
+                   z=None, want_out=True, want_ungated=False, want_h_last=True, want_ckpt=False):
+    """Fused forward with the optional transforms (delta' = softplus(delta + delta_bias),
+    out_z = out * silu(z)). Returns (out_z or out, ungated out or None, h_last or None, ckpt or None).
 
     ckpt is fp32 (B, ceil(L/16), D, 16): the state before every 16th step,
     which the backward restarts from."""
     check_ssm_inputs(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev)
+    check_transforms(u, delta_bias, z)
     u, delta, A, B_ssm, C_ssm, D_ssm = (t.contiguous() for t in (u, delta, A, B_ssm, C_ssm, D_ssm))
     h_prev = None if h_prev is None else h_prev.contiguous()
+    delta_bias = None if delta_bias is None else delta_bias.contiguous()
+    z = None if z is None else z.contiguous()
     L_ = _lib.lib()
     bsz, L, dm = u.shape
     dev = u.device
-    out = torch.empty_like(u) if want_out else None
+    gated = z is not None
+    out = torch.empty_like(u) if (want_out and not gated) or (gated and want_ungated) else None
+    out_z = torch.empty_like(u) if gated and want_out else None
     h_last = torch.empty(bsz, dm, NSTATE, dtype=u.dtype, device=dev) if want_h_last else None
     ckpt = (torch.empty(bsz, ckpt_count(L), dm, NSTATE, dtype=torch.float32, device=dev)
             if want_ckpt else None)
     nbytes = L_.mwc_ssm_fwd_workspace_size(bsz, L, dm, NSTATE)
     ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
-        st = L_.mwc_ssm_fwd(_dtype_code(u), _ptr(u), _ptr(delta), _ptr(A), _ptr(B_ssm), _ptr(C_ssm), _ptr(D_ssm),
-                            _ptr(h_prev), _ptr(out), _ptr(h_last), _ptr(ckpt), bsz, L, dm, NSTATE,
-                            ws.data_ptr(), nbytes, _stream(dev))
-    _lib.check(st, "mwc_ssm_fwd")
+        st = L_.mwc_ssm_fwd_ex(_dtype_code(u), _ptr(u), _ptr(delta), _ptr(A), _ptr(B_ssm), _ptr(C_ssm),
+                               _ptr(D_ssm), _ptr(h_prev), _ptr(delta_bias), int(bool(delta_softplus)), _ptr(z),
+                               _ptr(out), _ptr(out_z), _ptr(h_last), _ptr(ckpt), bsz, L, dm, NSTATE,
+                               ws.data_ptr(), nbytes, _stream(dev))
+    _lib.check(st, "mwc_ssm_fwd_ex")
+    return (out_z if gated else out), (out if gated else None), h_last, ckpt
+
+
+def ssm_forward(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, *, want_out=True, want_h_last=True,
+                want_ckpt=False):
+    """Fused forward. Returns (out or None, h_last or None, ckpt or None)."""
+    out, _, h_last, ckpt = ssm_forward_xf(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, want_out=want_out,
+                                          want_h_last=want_h_last, want_ckpt=want_ckpt)
     return out, h_last, ckpt
 
 
-def ssm_backward(u, delta, A, B_ssm, C_ssm, D_ssm, dout, ckpt, dh_last=None, want_dh_prev=False):
-    """Fused backward. Returns (du, ddelta, dA, dB, dC, dD, dh_prev or None), in u's dtype."""
+def ssm_backward_xf(u, delta, A, B_ssm, C_ssm, D_ssm, dout, ckpt, dh_last=None, want_dh_prev=False, *,
+                    delta_bias=None, delta_softplus=False, z=None, out_ungated=None):
+    """Fused backward with the optional transforms. With z, dout is the gradient of the gated
+    output and out_ungated the forward's ungated output. Returns
+    (du, ddelta, dA, dB, dC, dD, dh_prev or None, ddelta_bias or None, dz or None), in u's dtype."""
     u, delta, A, B_ssm, C_ssm, D_ssm = (t.contiguous() for t in (u, delta, A, B_ssm, C_ssm, D_ssm))
     bsz, L, dm = u.shape
     dout = dout.to(u.dtype).contiguous()
@@ -113,6 +142,13 @@ def ssm_backward(u, delta, A, B_ssm, C_ssm, D_ssm, dout, ckpt, dh_last=None, wan
         _require(tuple(dh_last.shape) == (bsz, dm, NSTATE), "dh_last shape must be (B, D, N)")
     _require(ckpt is not None and ckpt.dtype == torch.float32 and ckpt.is_contiguous()
              and tuple(ckpt.shape) == (bsz, ckpt_count(L), dm, NSTATE), "ckpt does not match the inputs")
+    check_transforms(u, delta_bias, z)
+    delta_bias = None if delta_bias is None else delta_bias.contiguous()
+    if z is not None:
+        z = z.contiguous()
+        _require(out_ungated is not None and tuple(out_ungated.shape) == (bsz, L, dm),
+                 "the ungated forward output is needed with z")
+        out_ungated = out_ungated.to(u.dtype).contiguous()
     L_ = _lib.lib()
     dev = u.device
     du = torch.empty_like(u)
@@ -122,15 +158,23 @@ def ssm_backward(u, delta, A, B_ssm, C_ssm, D_ssm, dout, ckpt, dh_last=None, wan
     dC = torch.empty_like(C_ssm)
     dD = torch.empty_like(D_ssm)
     dh_prev = torch.empty(bsz, dm, NSTATE, dtype=u.dtype, device=dev) if want_dh_prev else None
+    dbias = torch.empty_like(delta_bias) if delta_bias is not None else None
+    dz = torch.empty_like(z) if z is not None else None
     nbytes = L_.mwc_ssm_bwd_workspace_size(bsz, L, dm, NSTATE)
     ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
-        st = L_.mwc_ssm_bwd(_dtype_code(u), _ptr(u), _ptr(delta), _ptr(A), _ptr(B_ssm), _ptr(C_ssm), _ptr(D_ssm),
-                            None, _ptr(dout), _ptr(dh_last), _ptr(ckpt), _ptr(du), _ptr(ddelta), _ptr(dA), _ptr(dB),
-                            _ptr(dC), _ptr(dD), _ptr(dh_prev), bsz, L, dm, NSTATE, ws.data_ptr(), nbytes,
-                            _stream(dev))
-    _lib.check(st, "mwc_ssm_bwd")
-    return du, ddelta, dA, dB, dC, dD, dh_prev
+        st = L_.mwc_ssm_bwd_ex(_dtype_code(u), _ptr(u), _ptr(delta), _ptr(A), _ptr(B_ssm), _ptr(C_ssm),
+                               _ptr(D_ssm), None, _ptr(delta_bias), int(bool(delta_softplus)), _ptr(z),
+                               _ptr(out_ungated if z is not None else None), _ptr(dout), _ptr(dh_last), _ptr(ckpt),
+                               _ptr(du), _ptr(ddelta), _ptr(dA), _ptr(dB), _ptr(dC), _ptr(dD), _ptr(dbias),
+                               _ptr(dz), _ptr(dh_prev), bsz, L, dm, NSTATE, ws.data_ptr(), nbytes, _stream(dev))
+    _lib.check(st, "mwc_ssm_bwd_ex")
+    return du, ddelta, dA, dB, dC, dD, dh_prev, dbias, dz
+
+
+def ssm_backward(u, delta, A, B_ssm, C_ssm, D_ssm, dout, ckpt, dh_last=None, want_dh_prev=False):
+    """Fused backward. Returns (du, ddelta, dA, dB, dC, dD, dh_prev or None), in u's dtype."""
+    return ssm_backward_xf(u, delta, A, B_ssm, C_ssm, D_ssm, dout, ckpt, dh_last, want_dh_prev)[:7]
 
 
 def _scan_view(x: torch.Tensor):

@@ -25,7 +25,7 @@ class FusedSelectiveScanFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dout, dh_last):
-        return (*_backward_impl(ctx, dout, dh_last), None)
+        return (*_backward_impl(ctx, dout, dh_last)[:7], None)
 
 
 class FusedSelectiveScan(torch.nn.Module):

@@ -10,6 +10,10 @@ Each function restates one reference function (file:line in
 * ``ssm_bwd``   -- autograd through ``selective_scan_ref`` (tests/test_selective_scan.py:361-364)
 * ``pscan_fwd`` -- ``parallel_scan_ref`` (mamba_windows_cuda/pscan.py:153-171)
 * ``pscan_bwd`` -- the adjoint of ``parallel_scan_ref``
+* ``ssm_fwd_xf`` / ``ssm_bwd_xf`` -- ``ssm_fwd`` / ``ssm_bwd`` composed with the elementwise
+  transforms a Mamba block applies around the scan (delta' = softplus(delta + delta_bias),
+  out_z = out * silu(z)); the reference has no counterpart (it rejects them), so these follow the
+  textbook definitions, and the chain rule is written out here in float64
 
 All arithmetic is float64 on the (dtype-rounded) inputs. Pins live in
 tests/test_oracle.py.
@@ -94,6 +98,52 @@ def ssm_bwd(u, delta, A, B, C, D, dout, h_prev=None, dh_last=None, clamp=False):
                            _p(h_prev), _p(dout), _p(dh_last), int(bool(clamp)),
                            _p(r["du"]), _p(r["ddelta"]), _p(r["dA"]), _p(r["dB"]), _p(r["dC"]),
                            _p(r["dD"]), _p(r["dh_prev"]))
+    return r
+
+
+def _softplus(x):
+    return np.where(x > 20.0, x, np.log1p(np.exp(np.minimum(x, 20.0))))
+
+
+def _sigmoid(x):
+    return 1.0 / (1.0 + np.exp(-x))
+
+
+def _delta_xf(delta, delta_bias, delta_softplus):
+    d = _f64(delta)
+    if delta_bias is not None:
+        d = d + _f64(delta_bias)[None, None, :]
+    return _softplus(d) if delta_softplus else d, d
+
+
+def ssm_fwd_xf(u, delta, A, B, C, D, h_prev=None, delta_bias=None, delta_softplus=False, z=None, clamp=False):
+    """Returns (out_z or out, h_last, ungated out) in float64."""
+    dxf, _ = _delta_xf(delta, delta_bias, delta_softplus)
+    out, h_last = ssm_fwd(u, dxf, A, B, C, D, h_prev, clamp)
+    if z is None:
+        return out, h_last, out
+    zz = _f64(z)
+    return out * zz * _sigmoid(zz), h_last, out
+
+
+def ssm_bwd_xf(u, delta, A, B, C, D, dout, h_prev=None, dh_last=None, delta_bias=None, delta_softplus=False,
+               z=None, clamp=False):
+    """ssm_bwd through the transforms. Returns the ssm_bwd dict (ddelta w.r.t. the raw delta) plus
+    'ddelta_bias' and 'dz' (None when the transform is absent)."""
+    dxf, dpre = _delta_xf(delta, delta_bias, delta_softplus)
+    g = _f64(dout)
+    dz = None
+    if z is not None:
+        zz = _f64(z)
+        sz = _sigmoid(zz)
+        y, _ = ssm_fwd(u, dxf, A, B, C, D, h_prev, clamp)
+        dz = g * y * sz * (1.0 + zz * (1.0 - sz))
+        g = g * zz * sz
+    r = ssm_bwd(u, dxf, A, B, C, D, g, h_prev, dh_last, clamp)
+    if delta_softplus:
+        r["ddelta"] = r["ddelta"] * _sigmoid(dpre)
+    r["ddelta_bias"] = r["ddelta"].sum(axis=(0, 1)) if delta_bias is not None else None
+    r["dz"] = dz
     return r
 
 

@@ -68,6 +68,36 @@ def test_argument_errors_before_any_launch():
     assert L.mwc_pscan_fwd(0, None, None, None, 0, 8, 8, None, 0, None) == 0
 
 
+def test_transform_entry_points_argument_errors():
+    """The fused-transform entry points reject inconsistent optional arguments before any launch."""
+    from mamba_windows_cuda import _lib
+
+    L = _lib.lib()
+    fake = ctypes.c_void_p(16)
+    # out_z without z
+    st = L.mwc_ssm_fwd_ex(0, fake, fake, fake, fake, fake, fake, None, None, 0, None, fake, fake, None, None,
+                          1, 8, 8, 16, fake, 1 << 20, None)
+    assert st == 1 and b"out_z" in L.mwc_last_error()
+    # backward with z but no ungated output
+    st = L.mwc_ssm_bwd_ex(0, fake, fake, fake, fake, fake, fake, None, None, 0, fake, None, fake, None, fake,
+                          fake, fake, fake, fake, fake, fake, None, fake, None, 1, 8, 8, 16, fake, 1 << 20, None)
+    assert st == 1 and b"ungated" in L.mwc_last_error()
+    # ddelta_bias without delta_bias
+    st = L.mwc_ssm_bwd_ex(0, fake, fake, fake, fake, fake, fake, None, None, 0, None, None, fake, None, fake,
+                          fake, fake, fake, fake, fake, fake, fake, None, None, 1, 8, 8, 16, fake, 1 << 20, None)
+    assert st == 1
+
+
+def test_transform_validation():
+    from mamba_windows_cuda import ops
+
+    u = torch.randn(2, 5, 3)
+    with pytest.raises(RuntimeError, match="delta_bias shape"):
+        ops.check_transforms(u, torch.randn(4), None)
+    with pytest.raises(RuntimeError, match="z dtype"):
+        ops.check_transforms(u, None, torch.randn(2, 5, 3).double())
+
+
 def test_workspace_sizes_monotone():
     from mamba_windows_cuda import _lib
 

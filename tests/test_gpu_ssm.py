@@ -112,6 +112,74 @@ def test_segmented_clamp_path(dev, monkeypatch):
     _close("dh_prev", g["h_prev"], r["dh_prev"], torch.float32)
 
 
+def _run_xf(x, dev, *, bias, softplus, gate, lvl=0, dh_last=None):
+    """forward_with_state with the fused transforms + backward; returns out, h_last, grads."""
+    names = ["u", "delta", "A", "B", "C", "D", "h_prev"] + (["delta_bias"] if bias else []) + (["z"] if gate else [])
+    leaves = {k: x[k].to(dev).requires_grad_(True) for k in names}
+    m = SelectiveScanCuda(checkpoint_lvl=lvl)
+    out, h_last = m.forward_with_state(leaves["u"], leaves["delta"], leaves["A"], leaves["B"], leaves["C"],
+                                       leaves["D"], leaves["h_prev"], z=leaves.get("z"),
+                                       delta_bias=leaves.get("delta_bias"), delta_softplus=softplus)
+    loss = (out.float() * x["dout"].to(dev).float()).sum()
+    if dh_last is not None:
+        loss = loss + (h_last.float() * dh_last.to(dev).float()).sum()
+    loss.backward()
+    torch.cuda.synchronize()
+    return out, h_last, {k: v.grad for k, v in leaves.items()}
+
+
+XF_CASES = [(True, True, True), (True, True, False), (False, False, True), (False, True, False)]
+
+
+@pytest.mark.parametrize("xf", XF_CASES)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("shape,nseg", [((2, 333, 200), "3"), ((1, 77, 70), None), ((3, 40, 2100), None)])
+def test_fused_transforms(dev, monkeypatch, xf, dtype, shape, nseg):
+    """delta' = softplus(delta + delta_bias) and out * silu(z) fused into the kernels: out, h_last and
+    every gradient (incl. delta_bias, z, h_prev) against the float64 oracle composed with the
+    transforms."""
+    bias, softplus, gate = xf
+    if nseg:
+        monkeypatch.setenv("MWC_NSEG", nseg)
+    B, L, D = shape
+    print(f"case transforms xf={xf} dtype={dtype} shape={shape} nseg={nseg}", flush=True)
+    x = workloads.ssm_inputs(B, L, D, dtype=torch.float32, h_prev=True, seed=B + L + D)
+    g = torch.Generator().manual_seed(7)
+    if softplus:  # raw delta around softplus^-1 of the usual range
+        x["delta"] = -4.0 + 2.0 * torch.randn(B, L, D, generator=g)
+    x["delta_bias"] = 0.5 * torch.randn(D, generator=g)
+    x["z"] = torch.randn(B, L, D, generator=g)
+    x = {k: v.to(dtype) for k, v in x.items()}
+    dhl = (0.5 * torch.randn(B, D, 16, generator=g)).to(dtype)
+    out, h_last, gr = _run_xf(x, dev, bias=bias, softplus=softplus, gate=gate, dh_last=dhl)
+    kw = dict(delta_bias=x["delta_bias"] if bias else None, delta_softplus=softplus, z=x["z"] if gate else None,
+              clamp=True)
+    ro, rh, _ = orc.ssm_fwd_xf(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["h_prev"], **kw)
+    _close("out", out, ro, dtype)
+    _close("h_last", h_last, rh, dtype)
+    r = orc.ssm_bwd_xf(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["dout"], x["h_prev"], dhl, **kw)
+    for k, name in GRADS + (("h_prev", "dh_prev"),):
+        _close(name, gr[k], r[name], dtype)
+    if bias:
+        _close("ddelta_bias", gr["delta_bias"], r["ddelta_bias"], dtype)
+    if gate:
+        _close("dz", gr["z"], r["dz"], dtype)
+
+
+def test_fused_transforms_levels_agree(dev):
+    """Checkpoint levels 0 and 1 give bitwise-equal results with all three transforms."""
+    x = workloads.ssm_inputs(2, 300, 96, dtype=torch.float32, h_prev=True, seed=9)
+    g = torch.Generator().manual_seed(8)
+    x["delta"] = -3.0 + torch.randn(2, 300, 96, generator=g)
+    x["delta_bias"] = torch.randn(96, generator=g)
+    x["z"] = torch.randn(2, 300, 96, generator=g)
+    o0, h0, g0 = _run_xf(x, dev, bias=True, softplus=True, gate=True, lvl=0)
+    o1, h1, g1 = _run_xf(x, dev, bias=True, softplus=True, gate=True, lvl=1)
+    assert torch.equal(o0, o1) and torch.equal(h0, h1)
+    for k in g0:
+        assert torch.equal(g0[k], g1[k]), k
+
+
 def test_checkpoint_levels_agree_bitwise(dev):
     x = workloads.ssm_inputs(2, 300, 96, dtype=torch.float32, h_prev=True, seed=5)
     _, _, g0 = _run(x, dev, with_h=True, lvl=0)

@@ -120,6 +120,41 @@ def test_bwd_matches_autograd(shape, with_h):
         np.testing.assert_allclose(r["dh_prev"], hpl.grad.numpy(), rtol=1e-10, atol=1e-12)
 
 
+@pytest.mark.parametrize("bias,softplus,gate", [(True, True, True), (False, True, False), (True, False, False),
+                                                (False, False, True)])
+def test_transforms_match_autograd(bias, softplus, gate):
+    """ssm_fwd_xf / ssm_bwd_xf against torch autograd through softplus(delta + bias), the
+    sequential restatement and silu(z) gating (torch.nn.functional library routines)."""
+    bsz, L, dm, n = 2, 11, 6, 16
+    u, delta, A, B, C, D, hp = _inputs(bsz, L, dm, n, seed=41)
+    g = torch.Generator().manual_seed(42)
+    raw = torch.randn(bsz, L, dm, generator=g, dtype=F64) * 2.0 - 1.0 if softplus else delta
+    db = 0.5 * torch.randn(dm, generator=g, dtype=F64) if bias else None
+    z = torch.randn(bsz, L, dm, generator=g, dtype=F64) if gate else None
+    dout = torch.randn(bsz, L, dm, generator=g, dtype=F64)
+    dhl = torch.randn(bsz, dm, n, generator=g, dtype=F64)
+    leaves = [x.clone().requires_grad_(True) for x in (u, raw, A, B, C, D, hp)]
+    dbl = db.clone().requires_grad_(True) if bias else None
+    zl = z.clone().requires_grad_(True) if gate else None
+    d = leaves[1] + dbl if bias else leaves[1]
+    if softplus:
+        d = torch.nn.functional.softplus(d)
+    out, hl = torch_ref.selective_scan_seq(leaves[0], d, *leaves[2:6], leaves[6])
+    if gate:
+        out = out * torch.nn.functional.silu(zl)
+    ((out * dout).sum() + (hl * dhl).sum()).backward()
+    o, h, _ = orc.ssm_fwd_xf(u, raw, A, B, C, D, hp, db, softplus, z)
+    np.testing.assert_allclose(o, out.detach().numpy(), rtol=1e-11, atol=1e-12)
+    np.testing.assert_allclose(h, hl.detach().numpy(), rtol=1e-11, atol=1e-12)
+    r = orc.ssm_bwd_xf(u, raw, A, B, C, D, dout, hp, dhl, db, softplus, z)
+    for name, leaf in zip(("du", "ddelta", "dA", "dB", "dC", "dD", "dh_prev"), leaves):
+        np.testing.assert_allclose(r[name], leaf.grad.numpy(), rtol=1e-10, atol=1e-12, err_msg=name)
+    if bias:
+        np.testing.assert_allclose(r["ddelta_bias"], dbl.grad.numpy(), rtol=1e-10, atol=1e-12)
+    if gate:
+        np.testing.assert_allclose(r["dz"], zl.grad.numpy(), rtol=1e-10, atol=1e-12)
+
+
 def test_bwd_finite_differences():
     """Central differences of the oracle's own forward pin its backward."""
     bsz, L, dm, n = 2, 6, 3, 4
