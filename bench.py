@@ -7,7 +7,7 @@ storage / fp32 compute, B=8, L=2048, D=1536, N=16; one step = fused forward
 all inputs resident in HBM. Prints ONE JSON line.
 
   python bench.py [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4a|cfg4b]
-                  [--level 0|1] [--skip-cpu]
+                  [--level 0|1] [--skip-cpu] [--transforms]
 
 `value` = B*L*D / ms_per_step (elements/s). `roofline` covers the dominant
 kernel (the fused backward call), timed live with HIP events on the stream
@@ -137,6 +137,55 @@ def bench_ssm(cfg, steps, warmup, level):
     return res
 
 
+def bench_transforms(cfg, steps, warmup):
+    """A Mamba block's scan call: delta' = softplus(delta + delta_bias) and out * silu(z) fused into the
+    kernels, against the same step with the transforms as separate torch elementwise passes around
+    the plain fused scan. Both are fwd + bwd through autograd with all six gradients plus
+    d(delta_bias) and dz."""
+    import torch
+
+    from mamba_windows_cuda import SelectiveScanCuda, workloads
+
+    c = workloads.CONFIGS[cfg]
+    B, L, D = c["B"], c["L"], c["D"]
+    x = workloads.config_inputs(cfg, device="cuda", gen_device="cuda")
+    g = torch.Generator(device="cuda").manual_seed(1)
+    x["delta"] = (-4.0 + torch.randn(B, L, D, generator=g, device="cuda")).to(c["dtype"])
+    x["delta_bias"] = (0.5 * torch.randn(D, generator=g, device="cuda")).to(c["dtype"])
+    x["z"] = torch.randn(B, L, D, generator=g, device="cuda").to(c["dtype"])
+    names = ("u", "delta", "A", "B", "C", "D", "delta_bias", "z")
+    leaves = {k: x[k].requires_grad_(True) for k in names}
+    dout = x["dout"]
+    m = SelectiveScanCuda()
+
+    def fused():
+        for t in leaves.values():
+            t.grad = None
+        out = m(leaves["u"], leaves["delta"], leaves["A"], leaves["B"], leaves["C"], leaves["D"],
+                z=leaves["z"], delta_bias=leaves["delta_bias"], delta_softplus=True)
+        torch.autograd.backward(out, dout)
+
+    def unfused():
+        for t in leaves.values():
+            t.grad = None
+        dl = torch.nn.functional.softplus(leaves["delta"] + leaves["delta_bias"])
+        y = m(leaves["u"], dl, leaves["A"], leaves["B"], leaves["C"], leaves["D"])
+        torch.autograd.backward(y * torch.nn.functional.silu(leaves["z"]), dout)
+
+    res = {"metric": "fwd+bwd elements/sec (B·L·D), Mamba-block scan call with delta_bias + softplus + z gating",
+           "unit": "elements/s", "dtype": "f32", "storage_dtype": "f16" if c["dtype"] == torch.float16 else "f32",
+           "config": {"workload": f"{cfg} + fused transforms, B={B} L={L} D={D} N=16", "B": B, "L": L, "D": D}}
+    for name, fn in (("fused", fused), ("unfused_torch_elementwise", unfused)):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        ms = _events_ms(fn, steps)
+        res[name] = {"ms_per_step": ms, "elements_per_s": B * L * D / (ms * 1e-3)}
+    res["value"] = res["fused"]["elements_per_s"]
+    res["ms_per_step"] = res["fused"]["ms_per_step"]
+    return res
+
+
 def bench_pscan(steps, warmup):
     import torch
 
@@ -261,6 +310,8 @@ def main():
     ap.add_argument("--config", default="cfg2", choices=["cfg2", "cfg3", "cfg4a", "cfg4b"])
     ap.add_argument("--level", type=int, default=0, choices=[0, 1])
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--transforms", action="store_true",
+                    help="time the scan call with delta_bias/softplus/z gating fused vs. as torch passes")
     ap.add_argument("--kernels-only", action="store_true",
                     help="profiling driver: fused calls, cfg4b scan and a 1 GiB copy; no timing")
     args = ap.parse_args()
@@ -276,7 +327,10 @@ def main():
     if args.kernels_only:
         print(json.dumps(kernels_only(args.config if args.config in ("cfg2", "cfg3") else "cfg2")))
         return
-    if args.config == "cfg4b":
+    if args.transforms:
+        res = bench_transforms(args.config if args.config in ("cfg2", "cfg3") else "cfg2", args.steps, args.warmup)
+        args.skip_cpu = True
+    elif args.config == "cfg4b":
         res = bench_pscan(args.steps, args.warmup)
     elif args.config == "cfg4a":
         res = bench_stream(args.steps, args.warmup)

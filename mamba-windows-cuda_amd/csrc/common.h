@@ -55,9 +55,20 @@ template <> __device__ __forceinline__ void buf_st<half_t>(rsrc_t r, uint32_t of
     __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, static_cast<half_t>(v)), r, off, 0, 0);
 }
 
-// Elementwise transforms around the scan (OCML expf/log1pf; fp32).
-__device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log1pf(expf(x)); }
-__device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + expf(-x)); }
+// Elementwise transforms around the scan, from the hardware base-2 exp/log and reciprocal
+// (each ~1 ulp). softplus(x) = ln(1 + e^x): x itself above 20 (as torch's threshold), the series
+// t - t^2/2 + t^3/3 for t = e^x < 2^-6 (where 1 + t would round away t's low bits; the first
+// omitted term is below 2^-20 relative), else ln2 * log2(1 + t).
+constexpr float kLn2 = 0.6931471805599453f;
+__device__ __forceinline__ float softplus_f(float x) {
+    const float t = __builtin_amdgcn_exp2f(x * kLog2e);
+    const float series = t * __builtin_fmaf(t, __builtin_fmaf(t, 1.f / 3.f, -0.5f), 1.f);
+    const float big = kLn2 * __builtin_amdgcn_logf(1.f + t);
+    return x > 20.f ? x : (t < 0.015625f ? series : big);
+}
+__device__ __forceinline__ float sigmoid_f(float x) {
+    return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * kLog2e));
+}
 
 // DPP lane exchanges within 16-lane rows (gfx9 DPP controls).
 template <int CTRL> __device__ __forceinline__ float dpp(float v) {
