@@ -7,7 +7,7 @@ storage / fp32 compute, B=8, L=2048, D=1536, N=16; one step = fused forward
 all inputs resident in HBM. Prints ONE JSON line.
 
   python bench.py [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4a|cfg4b]
-                  [--level 0|1] [--skip-cpu] [--transforms]
+                  [--level 0|1] [--skip-cpu] [--transforms] [--decode [BATCH]]
 
 `value` = B*L*D / ms_per_step (elements/s). `roofline` covers the dominant
 kernel (the fused backward call), timed live with HIP events on the stream
@@ -186,6 +186,47 @@ def bench_transforms(cfg, steps, warmup):
     return res
 
 
+def bench_decode(cfg, steps, warmup, batch=None):
+    """Decode steps (L = 1, state carried in place) at the config's D and dtype. Bytes per step:
+    the state read and written (2*B*D*16*s) plus u, delta, out (3*B*D*s), B, C (2*B*16*s), A, D."""
+    import torch
+
+    from mamba_windows_cuda import SelectiveScanCuda, workloads
+
+    c = workloads.CONFIGS[cfg]
+    B, D = batch or c["B"], c["D"]
+    x = workloads.ssm_inputs(B, 1, D, dtype=c["dtype"], h_prev=True, dout=False, device="cuda", gen_device="cuda")
+    s = 2 if c["dtype"] == torch.float16 else 4
+    m = SelectiveScanCuda()
+    h = x["h_prev"].clone()
+    args = (x["u"][:, 0].contiguous(), x["delta"][:, 0].contiguous(), x["A"], x["B"][:, 0].contiguous(),
+            x["C"][:, 0].contiguous(), x["D"])
+
+    def step():
+        m.step(*args, h, out_state=h)
+
+    with torch.no_grad():
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        ms_eager = _events_ms(step, max(steps, 100))
+        # a decode loop as a serving engine runs it: 32 steps captured once in a HIP graph, replayed
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(32):
+                step()
+        graph.replay()
+        torch.cuda.synchronize()
+        ms = _events_ms(graph.replay, max(steps // 32, 10)) / 32
+    nbytes = s * (2 * B * D * 16 + 3 * B * D + 2 * B * 16 + D * 16 + D)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"metric": "decode steps/s (L=1, state in place, HIP-graph replay)", "value": 1e3 / ms,
+            "unit": "steps/s", "us_per_step": ms * 1e3, "us_per_step_eager": ms_eager * 1e3, "dtype": "f32", "storage_dtype": "f16" if s == 2 else "f32",
+            "config": {"workload": f"{cfg} decode step, B={B} D={D} N=16", "B": B, "D": D, "N": 16},
+            "roofline": {"bound": "hbm", "kernel": "ssm_step_kernel", "achieved": gbs, "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "algorithmic_bytes_per_launch": nbytes}}
+
+
 def bench_pscan(steps, warmup):
     import torch
 
@@ -310,6 +351,8 @@ def main():
     ap.add_argument("--config", default="cfg2", choices=["cfg2", "cfg3", "cfg4a", "cfg4b"])
     ap.add_argument("--level", type=int, default=0, choices=[0, 1])
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--decode", type=int, nargs="?", const=0, default=None, metavar="BATCH",
+                    help="time the L=1 decode step at the config's D (batch defaults to the config's)")
     ap.add_argument("--transforms", action="store_true",
                     help="time the scan call with delta_bias/softplus/z gating fused vs. as torch passes")
     ap.add_argument("--kernels-only", action="store_true",
@@ -327,7 +370,11 @@ def main():
     if args.kernels_only:
         print(json.dumps(kernels_only(args.config if args.config in ("cfg2", "cfg3") else "cfg2")))
         return
-    if args.transforms:
+    if args.decode is not None:
+        res = bench_decode(args.config if args.config in ("cfg2", "cfg3") else "cfg2", args.steps, args.warmup,
+                           args.decode or None)
+        args.skip_cpu = True
+    elif args.transforms:
         res = bench_transforms(args.config if args.config in ("cfg2", "cfg3") else "cfg2", args.steps, args.warmup)
         args.skip_cpu = True
     elif args.config == "cfg4b":

@@ -138,6 +138,19 @@ int mwc_ssm_bwd_ex(int dtype, const void* u, const void* delta, const void* A, c
                    void* ddelta_bias, void* dz, void* dh_prev, int64_t batch, int64_t seqlen, int64_t dim,
                    int64_t dstate, void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * One decode step (inference): mwc_ssm_fwd_ex at seqlen 1 with the state carried in and out, in a
+ * batched layout without the length axis:
+ *   u, delta, z, out, out_z (batch, dim); B_ssm, C_ssm (batch, 16); h, h_new (batch, dim, 16).
+ * h_new may alias h (in-place update). out may be NULL; out_z must be given with z (and only then).
+ * A, B_ssm, C_ssm, h and h_new must be aligned to 4 elements.
+ * Replaces selective_scan_cuda_forward_with_state (mamba_cuda.py:271-359) called with seqlen 1,
+ * the reference's only way to advance one step; needs no workspace.
+ */
+int mwc_ssm_step(int dtype, const void* u, const void* delta, const void* A, const void* B_ssm, const void* C_ssm,
+                 const void* D_ssm, const void* h, const void* delta_bias, int delta_softplus, const void* z,
+                 void* out, void* out_z, void* h_new, int64_t batch, int64_t dim, int64_t dstate, void* stream);
+
 size_t mwc_pscan_workspace_size(int64_t nseq, int64_t seqlen, int64_t ncols);
 
 /*

@@ -330,6 +330,26 @@ int mwc_ssm_bwd(int dtype, const void* u, const void* delta, const void* A, cons
                           workspace, workspace_bytes, stream);
 }
 
+int mwc_ssm_step(int dtype, const void* u, const void* delta, const void* A, const void* B_ssm, const void* C_ssm,
+                 const void* D_ssm, const void* h, const void* delta_bias, int delta_softplus, const void* z,
+                 void* out, void* out_z, void* h_new, int64_t batch, int64_t dim, int64_t dstate, void* stream) {
+    g_err[0] = 0;
+    if (int st = check_dims(dtype, batch, 1, dim, dstate)) return st;
+    if (batch == 0 || dim == 0) return MWC_OK;
+    if (!u || !delta || !A || !B_ssm || !C_ssm || !D_ssm || !h || !h_new)
+        return fail(MWC_ERR_INVALID_ARGUMENT, "u, delta, A, B_ssm, C_ssm, D_ssm, h and h_new must not be NULL");
+    if (z != nullptr && out_z == nullptr) return fail(MWC_ERR_INVALID_ARGUMENT, "out_z must not be NULL when z is given");
+    if (z == nullptr && out_z != nullptr) return fail(MWC_ERR_INVALID_ARGUMENT, "out_z needs z");
+    const uintptr_t align = 4 * (dtype == MWC_DTYPE_F16 ? 2 : 4);  // 4 states per vector access
+    for (const void* p : {A, B_ssm, C_ssm, h, static_cast<const void*>(h_new)})
+        if ((uintptr_t)p % align != 0)
+            return fail(MWC_ERR_INVALID_ARGUMENT, "A, B_ssm, C_ssm, h and h_new must be aligned to 4 elements");
+    MWC_HIP_TRY(mwc::launch_ssm_step(dtype == MWC_DTYPE_F16, u, delta, A, B_ssm, C_ssm, D_ssm, h,
+                                     mwc::ScanXf{delta_bias, z, delta_softplus != 0}, out, out_z, h_new, batch, dim,
+                                     (hipStream_t)stream));
+    return MWC_OK;
+}
+
 size_t mwc_pscan_workspace_size(int64_t nseq, int64_t seqlen, int64_t ncols) {
     return mwc::pscan_workspace_bytes(nseq, seqlen, ncols);
 }

@@ -70,6 +70,11 @@ hipError_t launch_bwd_finish(bool is_half, const float* dbc_part, const float* d
                              const float* dD_part, const float* dbias_part, void* dB, void* dC, void* dA,
                              void* dD, void* dbias, int ngroups, int nrows, const SsmShape& s, hipStream_t st);
 
+// One decode step (ssm_step.hip): u, delta, z, y, y_z (batch, dim); B, C (batch, 16); h (batch, dim, 16).
+hipError_t launch_ssm_step(bool is_half, const void* u, const void* delta, const void* A, const void* B,
+                           const void* C, const void* Dv, const void* h_in, const ScanXf& xf, void* y, void* y_z,
+                           void* h_out, int64_t batch, int64_t dim, hipStream_t st);
+
 // "state groups across waves" kernels (ssm_v3.hip)
 int impl_choice();  // 2 = lane groups (default), 3 = state groups across waves
 size_t v3_bcp_bytes(const SsmShape& s);

@@ -44,6 +44,9 @@ _SIGNATURES = {
     # du, ddelta, dA, dB, dC, dD, ddelta_bias, dz, dh_prev, sizes, ws
     "mwc_ssm_bwd_ex": ([ctypes.c_int, P, P, P, P, P, P, P, P, ctypes.c_int, P, P, P, P, P, P, P, P, P, P, P, P, P,
                         P, I64, I64, I64, I64, P, SZ, P], ctypes.c_int),
+    # dtype, u, delta, A, B, C, D, h, delta_bias, softplus, z, out, out_z, h_new, batch, dim, dstate, stream
+    "mwc_ssm_step": ([ctypes.c_int, P, P, P, P, P, P, P, P, ctypes.c_int, P, P, P, P, I64, I64, I64, P],
+                     ctypes.c_int),
     "mwc_pscan_workspace_size": ([I64, I64, I64], SZ),
     "mwc_pscan_fwd": ([ctypes.c_int, P, P, P, I64, I64, I64, P, SZ, P], ctypes.c_int),
     "mwc_pscan_bwd": ([ctypes.c_int, P, P, P, P, P, I64, I64, I64, P, SZ, P], ctypes.c_int),

@@ -138,6 +138,17 @@ class SelectiveScanCuda(torch.nn.Module):
         return SelectiveScanCudaFunction.apply(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, self.checkpoint_lvl, z,
                                                delta_bias, delta_softplus)
 
+    def step(self, u, delta, A, B_ssm, C_ssm, D_ssm, h, *, z=None, delta_bias=None, delta_softplus=False,
+             out_state=None):
+        """One decode step (inference only; not in the reference, whose way to advance one token is
+        forward_with_state with L=1). u, delta, z: (B, D); B_ssm, C_ssm: (B, N); h: (B, D, N).
+        Returns (out (B, D), h_new (B, D, N)); pass out_state=h to update the state in place."""
+        if torch.is_grad_enabled() and any(t is not None and t.requires_grad
+                                           for t in (u, delta, A, B_ssm, C_ssm, D_ssm, h, z, delta_bias)):
+            raise RuntimeError("SelectiveScanCuda.step is inference-only; use forward_with_state for gradients")
+        return ops.ssm_step(u, delta, A, B_ssm, C_ssm, D_ssm, h, delta_bias=delta_bias,
+                            delta_softplus=delta_softplus, z=z, out_state=out_state)
+
 
 def selective_scan_ref(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, return_intermediates=False):
     """Plain-PyTorch sequential selective scan (any device, autograd-capable),

@@ -177,6 +177,51 @@ def ssm_backward(u, delta, A, B_ssm, C_ssm, D_ssm, dout, ckpt, dh_last=None, wan
     return ssm_backward_xf(u, delta, A, B_ssm, C_ssm, D_ssm, dout, ckpt, dh_last, want_dh_prev)[:7]
 
 
+def ssm_step(u, delta, A, B_ssm, C_ssm, D_ssm, h, *, delta_bias=None, delta_softplus=False, z=None,
+             out_state=None):
+    """One decode step: u, delta, z (B, D); A (D, 16); B_ssm, C_ssm (B, 16); D_ssm (D,); h (B, D, 16).
+    Returns (out (B, D) -- gated by silu(z) when z is given --, h_new (B, D, 16)). out_state, when
+    given, receives h_new and may be h itself (in-place update)."""
+    named = (("u", u), ("delta", delta), ("A", A), ("B_ssm", B_ssm), ("C_ssm", C_ssm), ("D_ssm", D_ssm), ("h", h))
+    for name, t in named:
+        _require(t.is_cuda, f"{name} must be a CUDA tensor")
+        _require(t.dtype == u.dtype, f"{name} dtype must match u dtype")
+    _require(u.dtype in (torch.float32, torch.float16), "u must be float32/float16")
+    _require(u.dim() == 2, "u must be 2D (batch, dim) for a step")
+    bsz, dm = u.shape
+    _require(A.dim() == 2 and A.size(1) == NSTATE, "Only N=16 is supported")
+    for name, t, shape in (("delta", delta, (bsz, dm)), ("A", A, (dm, NSTATE)), ("B_ssm", B_ssm, (bsz, NSTATE)),
+                           ("C_ssm", C_ssm, (bsz, NSTATE)), ("D_ssm", D_ssm, (dm,)), ("h", h, (bsz, dm, NSTATE)),
+                           ("delta_bias", delta_bias, (dm,)), ("z", z, (bsz, dm))):
+        if t is not None:
+            _require(tuple(t.shape) == shape, f"{name} shape must be {shape}")
+            _require(t.dtype == u.dtype and t.device == u.device, f"{name} must match u's dtype and device")
+    align = 4 * u.element_size()  # the kernel moves 4 states per vector access
+
+    def aligned(t):
+        t = t.contiguous()
+        return t if t.data_ptr() % align == 0 else t.clone()
+
+    u, delta, D_ssm = (t.contiguous() for t in (u, delta, D_ssm))
+    A, B_ssm, C_ssm, h = (aligned(t) for t in (A, B_ssm, C_ssm, h))
+    delta_bias = None if delta_bias is None else delta_bias.contiguous()
+    z = None if z is None else z.contiguous()
+    if out_state is None:
+        out_state = torch.empty_like(h)
+    _require(out_state.is_contiguous() and tuple(out_state.shape) == (bsz, dm, NSTATE) and out_state.dtype == u.dtype
+             and out_state.data_ptr() % align == 0,
+             "out_state must be a contiguous, 4-element-aligned (B, D, 16) tensor of u's dtype")
+    out = torch.empty_like(u)
+    L_ = _lib.lib()
+    with torch.cuda.device(u.device):
+        st = L_.mwc_ssm_step(_dtype_code(u), _ptr(u), _ptr(delta), _ptr(A), _ptr(B_ssm), _ptr(C_ssm), _ptr(D_ssm),
+                             _ptr(h), _ptr(delta_bias), int(bool(delta_softplus)), _ptr(z),
+                             None if z is not None else _ptr(out), _ptr(out) if z is not None else None,
+                             _ptr(out_state), bsz, dm, NSTATE, _stream(u.device))
+    _lib.check(st, "mwc_ssm_step")
+    return out, out_state
+
+
 def _scan_view(x: torch.Tensor):
     """(B, D, L, N) -> (B*D, L, N) and (B, L, C) -> itself; the scan runs over dim -2."""
     if x.dim() == 4:

@@ -98,6 +98,21 @@ def test_transform_validation():
         ops.check_transforms(u, None, torch.randn(2, 5, 3).double())
 
 
+def test_step_argument_errors():
+    from mamba_windows_cuda import _lib
+
+    L = _lib.lib()
+    fake = ctypes.c_void_p(16)
+    # missing state
+    st = L.mwc_ssm_step(0, fake, fake, fake, fake, fake, fake, None, None, 0, None, fake, None, fake, 2, 8, 16, None)
+    assert st == 1 and b"h_new" in L.mwc_last_error()
+    # z without out_z, N != 16
+    assert L.mwc_ssm_step(0, fake, fake, fake, fake, fake, fake, fake, None, 0, fake, fake, None, fake, 2, 8, 16,
+                          None) == 1
+    assert L.mwc_ssm_step(0, fake, fake, fake, fake, fake, fake, fake, None, 0, None, fake, None, fake, 2, 8, 8,
+                          None) == 1
+
+
 def test_workspace_sizes_monotone():
     from mamba_windows_cuda import _lib
 
@@ -152,6 +167,9 @@ def test_cpu_tensors_are_rejected_not_computed():
         FusedSelectiveScan(1).forward_with_state(x["u"], x["delta"], x["A"], x["B_ssm"], x["C_ssm"], x["D_ssm"])
     with pytest.raises(RuntimeError, match="CUDA"):
         parallel_scan_fn(torch.rand(1, 2, 8, 4), torch.rand(1, 2, 8, 4))
+    with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
+        SelectiveScanCuda().step(x["u"][:, 0], x["delta"][:, 0], x["A"], x["B_ssm"][:, 0], x["C_ssm"][:, 0],
+                                 x["D_ssm"], torch.zeros(2, 3, 16))
 
 
 def test_reference_api_functions_on_cpu():
