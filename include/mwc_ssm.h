@@ -14,8 +14,9 @@
  *    A, dA (D,N); B_ssm, C_ssm, dB, dC (B,L,N); D_ssm, dD (D,);
  *    h_prev, h_last, dh_last, dh_prev (B,D,N).
  *  - dtype selects the element type of every tensor argument: MWC_DTYPE_F32
- *    (float) or MWC_DTYPE_F16 (IEEE binary16). Arithmetic is fp32 throughout;
- *    fp16 is storage only, rounded to nearest-even on store (the reference's
+ *    (float), MWC_DTYPE_F16 (IEEE binary16) or MWC_DTYPE_BF16 (bfloat16; not in
+ *    the reference, which rejects it). Arithmetic is fp32 throughout; fp16 and
+ *    bf16 are storage only, rounded to nearest-even on store (the reference's
  *    load_to_float/store_from_float, mamba_cuda.py:72-90).
  *  - N (dstate) must be 16 (mamba_cuda.py:215).
  *  - Work is enqueued on `stream` (a hipStream_t; NULL = default stream);
@@ -41,7 +42,7 @@ extern "C" {
  * the backward. */
 #define MWC_CKPT_STEPS 16
 
-enum mwc_dtype { MWC_DTYPE_F32 = 0, MWC_DTYPE_F16 = 1 };
+enum mwc_dtype { MWC_DTYPE_F32 = 0, MWC_DTYPE_F16 = 1, MWC_DTYPE_BF16 = 2 };
 
 enum mwc_status {
     MWC_OK = 0,

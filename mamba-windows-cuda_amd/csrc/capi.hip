@@ -33,8 +33,9 @@ int fail(int status, const char* fmt, ...) {
 }
 
 int check_dims(int dtype, int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate) {
-    if (dtype != MWC_DTYPE_F32 && dtype != MWC_DTYPE_F16)
-        return fail(MWC_ERR_INVALID_ARGUMENT, "dtype must be MWC_DTYPE_F32 or MWC_DTYPE_F16 (got %d)", dtype);
+    if (dtype != MWC_DTYPE_F32 && dtype != MWC_DTYPE_F16 && dtype != MWC_DTYPE_BF16)
+        return fail(MWC_ERR_INVALID_ARGUMENT, "dtype must be MWC_DTYPE_F32, MWC_DTYPE_F16 or MWC_DTYPE_BF16 (got %d)",
+                    dtype);
     if (dstate != mwc::kNState) return fail(MWC_ERR_INVALID_ARGUMENT, "Only N=16 is supported (got N=%lld)", (long long)dstate);
     if (batch < 0 || seqlen < 0 || dim < 0)
         return fail(MWC_ERR_INVALID_ARGUMENT, "negative size (batch=%lld, seqlen=%lld, dim=%lld)", (long long)batch,
@@ -231,7 +232,8 @@ int mwc_ssm_fwd_ex(int dtype, const void* u, const void* delta, const void* A, c
     if (seqlen > 0 && need > 0 && (workspace == nullptr || workspace_bytes < need))
         return fail(MWC_ERR_WORKSPACE, "forward workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
     if (mwc::impl_choice() == 3) {
-        if (xf) return fail(MWC_ERR_UNSUPPORTED, "delta_bias, delta_softplus and z need the default kernels");
+        if (xf || dtype == MWC_DTYPE_BF16)
+            return fail(MWC_ERR_UNSUPPORTED, "delta_bias, delta_softplus, z and bf16 need the default kernels");
         float* bcp = (float*)workspace;
         if (seqlen > 0) MWC_HIP_TRY(mwc::launch_v3_pack(half, B_ssm, C_ssm, bcp, s, st));
         MWC_HIP_TRY(mwc::launch_v3_fwd(half, u, delta, A, bcp, D_ssm, h_prev, out, h_last, ckpt, s, st));
@@ -242,7 +244,7 @@ int mwc_ssm_fwd_ex(int dtype, const void* u, const void* delta, const void* A, c
     float* car_x = (float*)((char*)workspace + need / 2);
     const mwc::FwdArgs a{u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, out, h_last, ckpt, car_h, car_x,
                          p.nseg, p.cps, p.cfold, p.ncar, mwc::ScanXf{delta_bias, z, delta_softplus != 0}, out_z};
-    MWC_HIP_TRY(mwc::launch_ssm_fwd(half, p.spl, a, s, st));
+    MWC_HIP_TRY(mwc::launch_ssm_fwd(dtype, p.spl, a, s, st));
     return MWC_OK;
 }
 
@@ -281,7 +283,8 @@ int mwc_ssm_bwd_ex(int dtype, const void* u, const void* delta, const void* A, c
     hipStream_t st = (hipStream_t)stream;
     char* w = (char*)workspace;
     if (mwc::impl_choice() == 3) {
-        if (xf) return fail(MWC_ERR_UNSUPPORTED, "delta_bias, delta_softplus and z need the default kernels");
+        if (xf || dtype == MWC_DTYPE_BF16)
+            return fail(MWC_ERR_UNSUPPORTED, "delta_bias, delta_softplus, z and bf16 need the default kernels");
         const int ngrp = mwc::v3_groups(s);
         float* bcp = (float*)w;
         w += mwc::v3_bcp_bytes(s);
@@ -293,7 +296,7 @@ int mwc_ssm_bwd_ex(int dtype, const void* u, const void* delta, const void* A, c
         if (seqlen > 0) MWC_HIP_TRY(mwc::launch_v3_pack(half, B_ssm, C_ssm, bcp, s, st));
         MWC_HIP_TRY(mwc::launch_v3_bwd(half, u, delta, A, bcp, D_ssm, dout, dh_last, ckpt, du, ddelta, dh_prev,
                                        dA_part, dD_part, dbc_part, s, st));
-        MWC_HIP_TRY(mwc::launch_bwd_finish(half, dbc_part, dA_part, dD_part, nullptr, dB, dC, dA, dD, nullptr, ngrp,
+        MWC_HIP_TRY(mwc::launch_bwd_finish(dtype, dbc_part, dA_part, dD_part, nullptr, dB, dC, dA, dD, nullptr, ngrp,
                                            (int)batch, s, st));
         return MWC_OK;
     }
@@ -313,8 +316,8 @@ int mwc_ssm_bwd_ex(int dtype, const void* u, const void* delta, const void* A, c
     const mwc::BwdArgs a{u, delta, A, B_ssm, C_ssm, D_ssm, dout, dh_last, ckpt, du, ddelta, dh_prev,
                          dA_part, dD_part, dbc_part, car_g, car_x, p.nseg, p.cps, p.cfold, p.ncar,
                          mwc::ScanXf{delta_bias, z, delta_softplus != 0}, out, dz, dbias_part};
-    MWC_HIP_TRY(mwc::launch_ssm_bwd(half, p.spl, a, s, st));
-    MWC_HIP_TRY(mwc::launch_bwd_finish(half, dbc_part, dA_part, dD_part, dbias_part, dB, dC, dA, dD,
+    MWC_HIP_TRY(mwc::launch_ssm_bwd(dtype, p.spl, a, s, st));
+    MWC_HIP_TRY(mwc::launch_bwd_finish(dtype, dbc_part, dA_part, dD_part, dbias_part, dB, dC, dA, dD,
                                        delta_bias != nullptr ? ddelta_bias : nullptr, ngrp, p.nseg * (int)batch, s,
                                        st));
     return MWC_OK;
@@ -344,7 +347,7 @@ int mwc_ssm_step(int dtype, const void* u, const void* delta, const void* A, con
     for (const void* p : {A, B_ssm, C_ssm, h, static_cast<const void*>(h_new)})
         if ((uintptr_t)p % align != 0)
             return fail(MWC_ERR_INVALID_ARGUMENT, "A, B_ssm, C_ssm, h and h_new must be aligned to 4 elements");
-    MWC_HIP_TRY(mwc::launch_ssm_step(dtype == MWC_DTYPE_F16, u, delta, A, B_ssm, C_ssm, D_ssm, h,
+    MWC_HIP_TRY(mwc::launch_ssm_step(dtype, u, delta, A, B_ssm, C_ssm, D_ssm, h,
                                      mwc::ScanXf{delta_bias, z, delta_softplus != 0}, out, out_z, h_new, batch, dim,
                                      (hipStream_t)stream));
     return MWC_OK;
@@ -355,8 +358,9 @@ size_t mwc_pscan_workspace_size(int64_t nseq, int64_t seqlen, int64_t ncols) {
 }
 
 static int check_pscan(int dtype, int64_t nseq, int64_t seqlen, int64_t ncols) {
-    if (dtype != MWC_DTYPE_F32 && dtype != MWC_DTYPE_F16)
-        return fail(MWC_ERR_INVALID_ARGUMENT, "dtype must be MWC_DTYPE_F32 or MWC_DTYPE_F16 (got %d)", dtype);
+    if (dtype != MWC_DTYPE_F32 && dtype != MWC_DTYPE_F16 && dtype != MWC_DTYPE_BF16)
+        return fail(MWC_ERR_INVALID_ARGUMENT, "dtype must be MWC_DTYPE_F32, MWC_DTYPE_F16 or MWC_DTYPE_BF16 (got %d)",
+                    dtype);
     if (nseq < 0 || seqlen < 0 || ncols < 0)
         return fail(MWC_ERR_INVALID_ARGUMENT, "negative size (nseq=%lld, seqlen=%lld, ncols=%lld)", (long long)nseq,
                     (long long)seqlen, (long long)ncols);
@@ -374,7 +378,7 @@ int mwc_pscan_fwd(int dtype, const void* A, const void* X, void* H, int64_t nseq
     const size_t need = mwc::pscan_workspace_bytes(nseq, seqlen, ncols);
     if (need && (workspace == nullptr || workspace_bytes < need))
         return fail(MWC_ERR_WORKSPACE, "scan workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
-    MWC_HIP_TRY(mwc::launch_pscan_fwd(dtype == MWC_DTYPE_F16, A, X, H, nseq, seqlen, ncols, workspace,
+    MWC_HIP_TRY(mwc::launch_pscan_fwd(dtype, A, X, H, nseq, seqlen, ncols, workspace,
                                       (hipStream_t)stream));
     return MWC_OK;
 }
@@ -388,7 +392,7 @@ int mwc_pscan_bwd(int dtype, const void* A, const void* H, const void* dH, void*
     const size_t need = mwc::pscan_workspace_bytes(nseq, seqlen, ncols);
     if (need && (workspace == nullptr || workspace_bytes < need))
         return fail(MWC_ERR_WORKSPACE, "scan workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
-    MWC_HIP_TRY(mwc::launch_pscan_bwd(dtype == MWC_DTYPE_F16, A, H, dH, dA, dX, nseq, seqlen, ncols, workspace,
+    MWC_HIP_TRY(mwc::launch_pscan_bwd(dtype, A, H, dH, dA, dX, nseq, seqlen, ncols, workspace,
                                       (hipStream_t)stream));
     return MWC_OK;
 }

@@ -14,6 +14,22 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kExp2Clamp = 88.0f * 1.4426950408889634f;
 
 typedef _Float16 half_t;
+typedef __bf16 bf16_t;  // storage only: converted to fp32 on load, rounded to nearest even on store
+
+// Storage dtype codes (mwc_dtype) and a dispatcher over the storage type.
+#define MWC_DISPATCH_DTYPE(dt, TT, ...)              \
+    do {                                               \
+        if ((dt) == MWC_DTYPE_F16) {                   \
+            typedef half_t TT;                         \
+            __VA_ARGS__;                               \
+        } else if ((dt) == MWC_DTYPE_BF16) {           \
+            typedef bf16_t TT;                         \
+            __VA_ARGS__;                               \
+        } else {                                       \
+            typedef float TT;                          \
+            __VA_ARGS__;                               \
+        }                                              \
+    } while (0)
 
 template <typename T> __device__ __forceinline__ float ld(const T* p) { return static_cast<float>(*p); }
 template <typename T> __device__ __forceinline__ void st(T* p, float v) { *p = static_cast<T>(v); }
@@ -39,6 +55,9 @@ template <> __device__ __forceinline__ float buf_ld<float>(rsrc_t r, uint32_t of
 template <> __device__ __forceinline__ float buf_ld<half_t>(rsrc_t r, uint32_t off) {
     return static_cast<float>(__builtin_bit_cast(half_t, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0)));
 }
+template <> __device__ __forceinline__ float buf_ld<bf16_t>(rsrc_t r, uint32_t off) {
+    return static_cast<float>(__builtin_bit_cast(bf16_t, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0)));
+}
 // Raw storage-type load (conversion deferred, keeps fp16 values in 16 bits while in flight).
 template <typename T> __device__ __forceinline__ T buf_raw(rsrc_t r, uint32_t off);
 template <> __device__ __forceinline__ float buf_raw<float>(rsrc_t r, uint32_t off) {
@@ -47,12 +66,18 @@ template <> __device__ __forceinline__ float buf_raw<float>(rsrc_t r, uint32_t o
 template <> __device__ __forceinline__ half_t buf_raw<half_t>(rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(half_t, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
 }
+template <> __device__ __forceinline__ bf16_t buf_raw<bf16_t>(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(bf16_t, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+}
 template <typename T> __device__ __forceinline__ void buf_st(rsrc_t r, uint32_t off, float v);
 template <> __device__ __forceinline__ void buf_st<float>(rsrc_t r, uint32_t off, float v) {
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, v), r, off, 0, 0);
 }
 template <> __device__ __forceinline__ void buf_st<half_t>(rsrc_t r, uint32_t off, float v) {
     __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, static_cast<half_t>(v)), r, off, 0, 0);
+}
+template <> __device__ __forceinline__ void buf_st<bf16_t>(rsrc_t r, uint32_t off, float v) {
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, static_cast<bf16_t>(v)), r, off, 0, 0);
 }
 
 // Elementwise transforms around the scan, from the hardware base-2 exp/log and reciprocal

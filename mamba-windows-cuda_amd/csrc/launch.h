@@ -61,17 +61,17 @@ struct BwdArgs {
     float* dbias_part;         // [nseg][batch][dim] delta_bias partials (xf.delta_bias != NULL)
 };
 
-// Kernel launchers; `is_half` selects fp16 storage. They only enqueue work.
-hipError_t launch_ssm_fwd(bool is_half, int spl, const FwdArgs& a, const SsmShape& s, hipStream_t st);
-hipError_t launch_ssm_bwd(bool is_half, int spl, const BwdArgs& a, const SsmShape& s, hipStream_t st);
+// Kernel launchers; `dt` is the storage dtype (mwc_dtype). They only enqueue work.
+hipError_t launch_ssm_fwd(int dt, int spl, const FwdArgs& a, const SsmShape& s, hipStream_t st);
+hipError_t launch_ssm_bwd(int dt, int spl, const BwdArgs& a, const SsmShape& s, hipStream_t st);
 // Sums the dB/dC partials of `ngroups` channel groups and the dA/dD (and, when dbias is not NULL,
 // delta_bias) partials of `nrows` rows.
-hipError_t launch_bwd_finish(bool is_half, const float* dbc_part, const float* dA_part,
+hipError_t launch_bwd_finish(int dt, const float* dbc_part, const float* dA_part,
                              const float* dD_part, const float* dbias_part, void* dB, void* dC, void* dA,
                              void* dD, void* dbias, int ngroups, int nrows, const SsmShape& s, hipStream_t st);
 
 // One decode step (ssm_step.hip): u, delta, z, y, y_z (batch, dim); B, C (batch, 16); h (batch, dim, 16).
-hipError_t launch_ssm_step(bool is_half, const void* u, const void* delta, const void* A, const void* B,
+hipError_t launch_ssm_step(int dt, const void* u, const void* delta, const void* A, const void* B,
                            const void* C, const void* Dv, const void* h_in, const ScanXf& xf, void* y, void* y_z,
                            void* h_out, int64_t batch, int64_t dim, hipStream_t st);
 
@@ -89,9 +89,9 @@ hipError_t launch_v3_bwd(bool is_half, const void* u, const void* delta, const v
                          void* ddelta, void* dh_prev, float* dA_part, float* dD_part, float* dbc_part,
                          const SsmShape& s, hipStream_t st);
 
-hipError_t launch_pscan_fwd(bool is_half, const void* A, const void* X, void* H, int64_t nseq,
+hipError_t launch_pscan_fwd(int dt, const void* A, const void* X, void* H, int64_t nseq,
                             int64_t seqlen, int64_t ncols, void* ws, hipStream_t st);
-hipError_t launch_pscan_bwd(bool is_half, const void* A, const void* H, const void* dH, void* dA,
+hipError_t launch_pscan_bwd(int dt, const void* A, const void* H, const void* dH, void* dA,
                             void* dX, int64_t nseq, int64_t seqlen, int64_t ncols, void* ws,
                             hipStream_t st);
 size_t pscan_workspace_bytes(int64_t nseq, int64_t seqlen, int64_t ncols);

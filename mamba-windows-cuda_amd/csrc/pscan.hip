@@ -206,16 +206,14 @@ static hipError_t pscan_t(const void* A, const void* X, const void* Hs, void* Ou
     return hipGetLastError();
 }
 
-hipError_t launch_pscan_fwd(bool is_half, const void* A, const void* X, void* H, int64_t nseq, int64_t seqlen,
+hipError_t launch_pscan_fwd(int dt, const void* A, const void* X, void* H, int64_t nseq, int64_t seqlen,
                             int64_t ncols, void* ws, hipStream_t st) {
-    return is_half ? pscan_t<half_t, false>(A, X, nullptr, H, nullptr, nseq, seqlen, ncols, ws, st)
-                   : pscan_t<float, false>(A, X, nullptr, H, nullptr, nseq, seqlen, ncols, ws, st);
+    MWC_DISPATCH_DTYPE(dt, TT, return pscan_t<TT, false>(A, X, nullptr, H, nullptr, nseq, seqlen, ncols, ws, st));
 }
 
-hipError_t launch_pscan_bwd(bool is_half, const void* A, const void* H, const void* dH, void* dA, void* dX,
+hipError_t launch_pscan_bwd(int dt, const void* A, const void* H, const void* dH, void* dA, void* dX,
                             int64_t nseq, int64_t seqlen, int64_t ncols, void* ws, hipStream_t st) {
-    return is_half ? pscan_t<half_t, true>(A, dH, H, dX, dA, nseq, seqlen, ncols, ws, st)
-                   : pscan_t<float, true>(A, dH, H, dX, dA, nseq, seqlen, ncols, ws, st);
+    MWC_DISPATCH_DTYPE(dt, TT, return pscan_t<TT, true>(A, dH, H, dX, dA, nseq, seqlen, ncols, ws, st));
 }
 
 }  // namespace mwc

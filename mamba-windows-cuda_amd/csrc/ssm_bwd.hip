@@ -706,9 +706,9 @@ static hipError_t bwd_inst(const BwdArgs& a, const SsmShape& s, hipStream_t st) 
     return xf ? bwd_inst<T, SPL, true>(a, s, st) : bwd_inst<T, SPL, false>(a, s, st);
 }
 
-hipError_t launch_ssm_bwd(bool is_half, int spl, const BwdArgs& a, const SsmShape& s, hipStream_t st) {
+hipError_t launch_ssm_bwd(int dt, int spl, const BwdArgs& a, const SsmShape& s, hipStream_t st) {
 #define MWC_BWD_SPL(S) \
-    if (spl == S) return is_half ? bwd_inst<half_t, S>(a, s, st) : bwd_inst<float, S>(a, s, st);
+    if (spl == S) MWC_DISPATCH_DTYPE(dt, TT, return bwd_inst<TT, S>(a, s, st));
     MWC_BWD_SPL(1)
     MWC_BWD_SPL(2)
     MWC_BWD_SPL(4)
@@ -730,13 +730,12 @@ static hipError_t finish_t(const float* dbc_part, const float* dA_part, const fl
     return hipGetLastError();
 }
 
-hipError_t launch_bwd_finish(bool is_half, const float* dbc_part, const float* dA_part, const float* dD_part,
+hipError_t launch_bwd_finish(int dt, const float* dbc_part, const float* dA_part, const float* dD_part,
                              const float* dbias_part, void* dB, void* dC, void* dA, void* dD, void* dbias,
                              int ngroups, int nrows, const SsmShape& s, hipStream_t st) {
-    return is_half ? finish_t<half_t>(dbc_part, dA_part, dD_part, dbias_part, dB, dC, dA, dD, dbias, ngroups, nrows,
-                                      s, st)
-                   : finish_t<float>(dbc_part, dA_part, dD_part, dbias_part, dB, dC, dA, dD, dbias, ngroups, nrows,
-                                     s, st);
+    MWC_DISPATCH_DTYPE(dt, TT,
+                       return finish_t<TT>(dbc_part, dA_part, dD_part, dbias_part, dB, dC, dA, dD, dbias, ngroups,
+                                           nrows, s, st));
 }
 
 }  // namespace mwc

@@ -324,9 +324,9 @@ static hipError_t fwd_inst(const FwdArgs& a, const SsmShape& s, hipStream_t st) 
     return xf ? fwd_inst<T, SPL, true>(a, s, st) : fwd_inst<T, SPL, false>(a, s, st);
 }
 
-hipError_t launch_ssm_fwd(bool is_half, int spl, const FwdArgs& a, const SsmShape& s, hipStream_t st) {
+hipError_t launch_ssm_fwd(int dt, int spl, const FwdArgs& a, const SsmShape& s, hipStream_t st) {
 #define MWC_FWD_SPL(S) \
-    if (spl == S) return is_half ? fwd_inst<half_t, S>(a, s, st) : fwd_inst<float, S>(a, s, st);
+    if (spl == S) MWC_DISPATCH_DTYPE(dt, TT, return fwd_inst<TT, S>(a, s, st));
     MWC_FWD_SPL(1)
     MWC_FWD_SPL(2)
     MWC_FWD_SPL(4)

@@ -64,21 +64,16 @@ __global__ void __launch_bounds__(256) ssm_step_kernel(const T* __restrict__ u, 
     }
 }
 
-hipError_t launch_ssm_step(bool is_half, const void* u, const void* delta, const void* A, const void* B,
-                           const void* C, const void* Dv, const void* h_in, const ScanXf& xf, void* y, void* y_z,
-                           void* h_out, int64_t batch, int64_t dim, hipStream_t st) {
+hipError_t launch_ssm_step(int dt, const void* u, const void* delta, const void* A, const void* B, const void* C,
+                           const void* Dv, const void* h_in, const ScanXf& xf, void* y, void* y_z, void* h_out,
+                           int64_t batch, int64_t dim, hipStream_t st) {
     const int64_t channels = batch * dim;
     const int64_t lanes = channels * kStepLpc;
     const int grid = (int)((lanes + 255) / 256);
-#define MWC_STEP(TT)                                                                                         \
-    hipLaunchKernelGGL(ssm_step_kernel<TT>, dim3(grid), dim3(256), 0, st, (const TT*)u, (const TT*)delta,     \
-                       (const TT*)A, (const TT*)B, (const TT*)C, (const TT*)Dv, (const TT*)h_in, xf, (TT*)y,  \
-                       (TT*)y_z, (TT*)h_out, channels, (int)dim)
-    if (is_half)
-        MWC_STEP(half_t);
-    else
-        MWC_STEP(float);
-#undef MWC_STEP
+    MWC_DISPATCH_DTYPE(dt, TT,
+                       hipLaunchKernelGGL(ssm_step_kernel<TT>, dim3(grid), dim3(256), 0, st, (const TT*)u,
+                                          (const TT*)delta, (const TT*)A, (const TT*)B, (const TT*)C, (const TT*)Dv,
+                                          (const TT*)h_in, xf, (TT*)y, (TT*)y_z, (TT*)h_out, channels, (int)dim));
     return hipGetLastError();
 }
 

@@ -17,6 +17,7 @@ LIB_PATH = os.environ.get("MWC_SSM_LIB", os.path.join(_HERE, "libmwc_ssm.so"))
 
 MWC_DTYPE_F32 = 0
 MWC_DTYPE_F16 = 1
+MWC_DTYPE_BF16 = 2
 MWC_OK = 0
 CKPT_STEPS = 16  # MWC_CKPT_STEPS
 

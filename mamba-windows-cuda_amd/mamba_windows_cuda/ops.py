@@ -17,8 +17,11 @@ from . import _lib
 NSTATE = 16
 
 
+STORAGE_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
+
+
 def _dtype_code(t: torch.Tensor) -> int:
-    return _lib.MWC_DTYPE_F16 if t.dtype == torch.float16 else _lib.MWC_DTYPE_F32
+    return {torch.float16: _lib.MWC_DTYPE_F16, torch.bfloat16: _lib.MWC_DTYPE_BF16}.get(t.dtype, _lib.MWC_DTYPE_F32)
 
 
 def _ptr(t):
@@ -40,7 +43,8 @@ def check_ssm_inputs(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, *, require_d
     if require_device:
         for name, t in named:
             _require(t.is_cuda, f"{name} must be a CUDA tensor")
-    _require(u.dtype in (torch.float32, torch.float16), "u must be float32/float16")
+    # bfloat16 is accepted in addition to the reference's float32/float16 (storage only, fp32 math)
+    _require(u.dtype in STORAGE_DTYPES, "u must be float32/float16 (or bfloat16)")
     for name, t in named[1:]:
         _require(t.dtype == u.dtype, f"{name} dtype must match u dtype")
     for name, t in named:
@@ -186,7 +190,7 @@ def ssm_step(u, delta, A, B_ssm, C_ssm, D_ssm, h, *, delta_bias=None, delta_soft
     for name, t in named:
         _require(t.is_cuda, f"{name} must be a CUDA tensor")
         _require(t.dtype == u.dtype, f"{name} dtype must match u dtype")
-    _require(u.dtype in (torch.float32, torch.float16), "u must be float32/float16")
+    _require(u.dtype in STORAGE_DTYPES, "u must be float32/float16 (or bfloat16)")
     _require(u.dim() == 2, "u must be 2D (batch, dim) for a step")
     bsz, dm = u.shape
     _require(A.dim() == 2 and A.size(1) == NSTATE, "Only N=16 is supported")
@@ -235,7 +239,7 @@ def _scan_view(x: torch.Tensor):
 def _check_scan(*ts):
     for t in ts:
         _require(t.is_cuda, "parallel_scan_fn inputs must be CUDA tensors")
-        _require(t.dtype in (torch.float32, torch.float16), "parallel_scan_fn supports float32/float16")
+        _require(t.dtype in STORAGE_DTYPES, "parallel_scan_fn supports float32/float16 (or bfloat16)")
         _require(t.dtype == ts[0].dtype and tuple(t.shape) == tuple(ts[0].shape),
                  "parallel_scan_fn inputs must share dtype and shape")
         _require(t.device == ts[0].device, "parallel_scan_fn inputs must share a device")

@@ -8,14 +8,15 @@ from oracle import oracle as orc
 
 pytestmark = pytest.mark.gpu
 
-TOL = {torch.float32: dict(rtol=1e-3, atol=1e-4), torch.float16: dict(rtol=1e-2, atol=1e-2)}
+TOL = {torch.float32: dict(rtol=1e-3, atol=1e-4), torch.float16: dict(rtol=1e-2, atol=1e-2),
+       torch.bfloat16: dict(rtol=2e-2, atol=2e-2)}
 
 
 def _np(t):
     return t.detach().cpu().double().numpy()
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("shape", [(2, 32, 128, 16), (1, 16, 64, 8), (3, 5, 1000, 3), (2, 1, 1, 7),
                                    (2, 777, 40), (1, 300, 1024), (2, 129, 64)])
 def test_pscan_forward_backward(dev, shape, dtype):

@@ -14,7 +14,9 @@ from oracle import oracle as orc
 
 pytestmark = pytest.mark.gpu
 
-TOL = {torch.float32: dict(rtol=1e-3, atol=1e-4), torch.float16: dict(rtol=1e-2, atol=1e-2)}
+# bf16 (8-bit mantissa; not in the reference) rounds outputs ~8x coarser than fp16: twice fp16's bound
+TOL = {torch.float32: dict(rtol=1e-3, atol=1e-4), torch.float16: dict(rtol=1e-2, atol=1e-2),
+       torch.bfloat16: dict(rtol=2e-2, atol=2e-2)}
 GRADS = (("u", "du"), ("delta", "ddelta"), ("A", "dA"), ("B", "dB"), ("C", "dC"), ("D", "dD"))
 
 
@@ -178,6 +180,36 @@ def test_fused_transforms_levels_agree(dev):
     assert torch.equal(o0, o1) and torch.equal(h0, h1)
     for k in g0:
         assert torch.equal(g0[k], g1[k]), k
+
+
+@pytest.mark.parametrize("shape,nseg", [((1, 77, 70), None), ((2, 333, 200), "3"), ((3, 40, 2100), None)])
+@pytest.mark.parametrize("xf", [False, True])
+def test_bfloat16(dev, monkeypatch, shape, nseg, xf):
+    """bf16 storage (fp32 math): out, h_last and every gradient against the float64 oracle on the
+    bf16-rounded inputs, with and without the fused transforms, split and unsplit."""
+    if nseg:
+        monkeypatch.setenv("MWC_NSEG", nseg)
+    B, L, D = shape
+    print(f"case bf16 shape={shape} nseg={nseg} xf={xf}", flush=True)
+    x = workloads.ssm_inputs(B, L, D, dtype=torch.float32, h_prev=True, seed=B * 7 + L + D)
+    g = torch.Generator().manual_seed(2)
+    x["delta_bias"] = 0.5 * torch.randn(D, generator=g)
+    x["z"] = torch.randn(B, L, D, generator=g)
+    if xf:
+        x["delta"] = -4.0 + 2.0 * torch.randn(B, L, D, generator=g)
+    x = {k: v.to(torch.bfloat16) for k, v in x.items()}
+    dhl = (0.5 * torch.randn(B, D, 16, generator=g)).to(torch.bfloat16)
+    out, h_last, gr = _run_xf(x, dev, bias=xf, softplus=xf, gate=xf, dh_last=dhl)
+    kw = dict(delta_bias=x["delta_bias"] if xf else None, delta_softplus=xf, z=x["z"] if xf else None, clamp=True)
+    ro, rh, _ = orc.ssm_fwd_xf(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["h_prev"], **kw)
+    _close("out", out, ro, torch.bfloat16)
+    _close("h_last", h_last, rh, torch.bfloat16)
+    r = orc.ssm_bwd_xf(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["dout"], x["h_prev"], dhl, **kw)
+    for k, name in GRADS + (("h_prev", "dh_prev"),):
+        _close(name, gr[k], r[name], torch.bfloat16)
+    if xf:
+        _close("ddelta_bias", gr["delta_bias"], r["ddelta_bias"], torch.bfloat16)
+        _close("dz", gr["z"], r["dz"], torch.bfloat16)
 
 
 def test_checkpoint_levels_agree_bitwise(dev):

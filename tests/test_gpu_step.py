@@ -11,7 +11,8 @@ from oracle import oracle as orc
 
 pytestmark = pytest.mark.gpu
 
-TOL = {torch.float32: dict(rtol=1e-3, atol=1e-4), torch.float16: dict(rtol=1e-2, atol=1e-2)}
+TOL = {torch.float32: dict(rtol=1e-3, atol=1e-4), torch.float16: dict(rtol=1e-2, atol=1e-2),
+       torch.bfloat16: dict(rtol=2e-2, atol=2e-2)}
 
 
 def _close(name, got, ref, dtype):
@@ -27,7 +28,7 @@ def _step_inputs(Bsz, D, dtype, seed):
     return {k: v.to(dtype) for k, v in x.items()}
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("shape", [(1, 70), (8, 1536), (3, 2100)])
 @pytest.mark.parametrize("xf", [False, True])
 def test_step_matches_oracle(dev, dtype, shape, xf):
