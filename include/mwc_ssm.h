@@ -18,7 +18,8 @@
  *    the reference, which rejects it). Arithmetic is fp32 throughout; fp16 and
  *    bf16 are storage only, rounded to nearest-even on store (the reference's
  *    load_to_float/store_from_float, mamba_cuda.py:72-90).
- *  - N (dstate) must be 16 (mamba_cuda.py:215).
+ *  - N (dstate) must be 16 (mamba_cuda.py:215) or, not in the reference, 8, 32
+ *    or 64.
  *  - Work is enqueued on `stream` (a hipStream_t; NULL = default stream);
  *    nothing synchronises the host. The library never allocates device
  *    memory: scratch space comes from the caller through `workspace`, whose
@@ -79,7 +80,7 @@ size_t mwc_ssm_fwd_workspace_size(int64_t batch, int64_t seqlen, int64_t dim, in
  *
  * out     may be NULL (state-only pass, used to regenerate checkpoints).
  * h_last  may be NULL.
- * ckpt    may be NULL; otherwise fp32 [batch][mwc_ssm_ckpt_count(seqlen)][dim][16]
+ * ckpt    may be NULL; otherwise fp32 [batch][mwc_ssm_ckpt_count(seqlen)][dim][N]
  *         receiving the state before steps 0, 16, 32, ... (checkpoint 0 = h_prev).
  */
 int mwc_ssm_fwd(int dtype, const void* u, const void* delta, const void* A, const void* B_ssm,
@@ -142,7 +143,7 @@ int mwc_ssm_bwd_ex(int dtype, const void* u, const void* delta, const void* A, c
 /*
  * One decode step (inference): mwc_ssm_fwd_ex at seqlen 1 with the state carried in and out, in a
  * batched layout without the length axis:
- *   u, delta, z, out, out_z (batch, dim); B_ssm, C_ssm (batch, 16); h, h_new (batch, dim, 16).
+ *   u, delta, z, out, out_z (batch, dim); B_ssm, C_ssm (batch, N); h, h_new (batch, dim, N).
  * h_new may alias h (in-place update). out may be NULL; out_z must be given with z (and only then).
  * A, B_ssm, C_ssm, h and h_new must be aligned to 4 elements.
  * Replaces selective_scan_cuda_forward_with_state (mamba_cuda.py:271-359) called with seqlen 1,

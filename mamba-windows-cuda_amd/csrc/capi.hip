@@ -36,7 +36,8 @@ int check_dims(int dtype, int64_t batch, int64_t seqlen, int64_t dim, int64_t ds
     if (dtype != MWC_DTYPE_F32 && dtype != MWC_DTYPE_F16 && dtype != MWC_DTYPE_BF16)
         return fail(MWC_ERR_INVALID_ARGUMENT, "dtype must be MWC_DTYPE_F32, MWC_DTYPE_F16 or MWC_DTYPE_BF16 (got %d)",
                     dtype);
-    if (dstate != mwc::kNState) return fail(MWC_ERR_INVALID_ARGUMENT, "Only N=16 is supported (got N=%lld)", (long long)dstate);
+    if (dstate != 8 && dstate != 16 && dstate != 32 && dstate != 64)
+        return fail(MWC_ERR_INVALID_ARGUMENT, "Only N=16 (or 8, 32, 64) is supported (got N=%lld)", (long long)dstate);
     if (batch < 0 || seqlen < 0 || dim < 0)
         return fail(MWC_ERR_INVALID_ARGUMENT, "negative size (batch=%lld, seqlen=%lld, dim=%lld)", (long long)batch,
                     (long long)seqlen, (long long)dim);
@@ -59,9 +60,20 @@ namespace mwc {
 // States per lane. Measured on MI355X at B=8, L=2048, D=1536 (fp16): SPL=2 (8 lanes per
 // channel) beats SPL=4 (one wave per SIMD, every stall exposed) and SPL=1 (4x the per-lane
 // overhead of the n-reductions). Small problems use SPL=1 for parallelism.
-int choose_spl(int64_t channels) {
-    if (const int o = spl_override()) return o;
-    return channels >= 2048 ? 2 : 1;
+int choose_spl(int64_t channels, int ns) {
+    const int o = spl_override();
+    if (o && lane_group_supported(ns, o)) return o;
+    // 8 lanes per channel (16 for small problems, for parallelism), within the built set
+    const int spl = ns / (channels >= 2048 ? 8 : 16);
+    return spl < 1 ? 1 : (ns == 64 ? 4 : spl);
+}
+
+bool lane_group_supported(int ns, int spl) {
+#define MWC_LG(N, S) \
+    if (ns == N && spl == S) return true;
+    MWC_FOR_EACH_LANE_GROUP(MWC_LG)
+#undef MWC_LG
+    return false;
 }
 
 namespace {
@@ -91,14 +103,14 @@ double pass_time(int64_t wgs, int64_t chunks, int cap) {
     return (double)r * ((double)chunks * q / simd_throughput(q) + 1.0);  // +1: prologue, first loads
 }
 
-int cpb_of(int spl) { return 4 * 64 / (kNState / spl); }
+int cpb_of(int ns, int spl) { return 4 * 64 / (ns / spl); }
 
 // Picks the segment count (and the carry split) minimising the modelled time of
 // carry pass + main pass. caps = workgroups per CU each kernel fits (registers, LDS);
 // carry_rel = cost of a carry-pass chunk relative to a main-pass chunk.
 SegPlan plan(const SsmShape& s, bool bwd, int spl, int cap_main, int cap_carry, double carry_rel) {
     const int64_t nck = (s.seqlen + kCkptSteps - 1) / kCkptSteps;
-    const int64_t w1 = s.batch * ((s.dim + cpb_of(spl) - 1) / cpb_of(spl));
+    const int64_t w1 = s.batch * ((s.dim + cpb_of(s.nstate, spl) - 1) / cpb_of(s.nstate, spl));
     SegPlan best{spl, 1, (int)nck, 1, 0};
     double best_t = pass_time(w1, nck, cap_main);
     // MWC_NSEG / MWC_CFOLD force the segment count / carry split (tuning and tests)
@@ -130,19 +142,22 @@ int bwd_cap(int spl) { return spl == 4 ? 1 : 3; }
 int bwd_carry_cap(int spl) { return spl == 1 ? 5 : spl == 2 ? 4 : 2; }
 
 size_t carry_bytes(const SsmShape& s, const SegPlan& p) {
-    return p.nseg > 1 ? align256((size_t)s.batch * p.ncar * s.dim * kNState * sizeof(float)) : 0;
+    return p.nseg > 1 ? align256((size_t)s.batch * p.ncar * s.dim * s.nstate * sizeof(float)) : 0;
 }
 
 }  // namespace
 
+// (the tables above are for N=16; other N get a conservative 2, which only steers the segment count)
 SegPlan plan_fwd(const SsmShape& s) {
-    const int spl = choose_spl(s.batch * s.dim);
-    return plan(s, false, spl, fwd_cap(spl), fwd_carry_cap(spl), 0.6);
+    const int spl = choose_spl(s.batch * s.dim, s.nstate);
+    const bool n16 = s.nstate == 16;
+    return plan(s, false, spl, n16 ? fwd_cap(spl) : 2, n16 ? fwd_carry_cap(spl) : 2, 0.6);
 }
 
 SegPlan plan_bwd(const SsmShape& s) {
-    const int spl = choose_spl(s.batch * s.dim);
-    return plan(s, true, spl, bwd_cap(spl), bwd_carry_cap(spl), 0.3);
+    const int spl = choose_spl(s.batch * s.dim, s.nstate);
+    const bool n16 = s.nstate == 16;
+    return plan(s, true, spl, n16 ? bwd_cap(spl) : 2, n16 ? bwd_carry_cap(spl) : 2, 0.3);
 }
 
 // Kernel family: 2 = lane groups (ssm_fwd.hip / ssm_bwd.hip, the default), 3 = state groups across
@@ -166,13 +181,14 @@ size_t bwd_workspace_bytes(const SsmShape& s) {
     if (impl_choice() == 3) {
         size_t n = v3_bcp_bytes(s);
         n += align256((size_t)v3_groups(s) * s.batch * s.seqlen * 32 * sizeof(float));
-        n += align256((size_t)s.batch * s.dim * kNState * sizeof(float));
+        n += align256((size_t)s.batch * s.dim * s.nstate * sizeof(float));
         n += align256((size_t)s.batch * s.dim * sizeof(float));
         return n;
     }
     const SegPlan p = plan_bwd(s);
-    size_t n = align256((size_t)bwd_groups(s, p.spl) * s.batch * s.seqlen * 32 * sizeof(float));  // dB/dC
-    n += align256((size_t)p.nseg * s.batch * s.dim * kNState * sizeof(float));                      // dA
+    size_t n = align256((size_t)bwd_groups(s, s.nstate, p.spl) * s.batch * s.seqlen * 2 * s.nstate *
+                        sizeof(float));                                                          // dB/dC
+    n += align256((size_t)p.nseg * s.batch * s.dim * s.nstate * sizeof(float));                  // dA
     n += align256((size_t)p.nseg * s.batch * s.dim * sizeof(float));                                // dD
     n += align256((size_t)p.nseg * s.batch * s.dim * sizeof(float));                                // d bias
     n += 2 * carry_bytes(s, p);
@@ -203,13 +219,11 @@ int64_t mwc_ssm_ckpt_count(int64_t seqlen) {
 }
 
 size_t mwc_ssm_fwd_workspace_size(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate) {
-    (void)dstate;
-    return mwc::fwd_workspace_bytes({batch, seqlen, dim});
+    return mwc::fwd_workspace_bytes({batch, seqlen, dim, (int)dstate});
 }
 
 size_t mwc_ssm_bwd_workspace_size(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate) {
-    (void)dstate;
-    return mwc::bwd_workspace_bytes({batch, seqlen, dim});
+    return mwc::bwd_workspace_bytes({batch, seqlen, dim, (int)dstate});
 }
 
 int mwc_ssm_fwd_ex(int dtype, const void* u, const void* delta, const void* A, const void* B_ssm,
@@ -225,15 +239,15 @@ int mwc_ssm_fwd_ex(int dtype, const void* u, const void* delta, const void* A, c
         return fail(MWC_ERR_INVALID_ARGUMENT, "u, delta, B_ssm and C_ssm must not be NULL");
     if (z == nullptr && out_z != nullptr) return fail(MWC_ERR_INVALID_ARGUMENT, "out_z needs z");
     const bool xf = delta_bias != nullptr || delta_softplus != 0 || z != nullptr;
-    const mwc::SsmShape s{batch, seqlen, dim};
+    const mwc::SsmShape s{batch, seqlen, dim, (int)dstate};
     const bool half = dtype == MWC_DTYPE_F16;
     hipStream_t st = (hipStream_t)stream;
     const size_t need = mwc::fwd_workspace_bytes(s);
     if (seqlen > 0 && need > 0 && (workspace == nullptr || workspace_bytes < need))
         return fail(MWC_ERR_WORKSPACE, "forward workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
     if (mwc::impl_choice() == 3) {
-        if (xf || dtype == MWC_DTYPE_BF16)
-            return fail(MWC_ERR_UNSUPPORTED, "delta_bias, delta_softplus, z and bf16 need the default kernels");
+        if (xf || dtype == MWC_DTYPE_BF16 || dstate != 16)
+            return fail(MWC_ERR_UNSUPPORTED, "delta_bias, delta_softplus, z, bf16 and N != 16 need the default kernels");
         float* bcp = (float*)workspace;
         if (seqlen > 0) MWC_HIP_TRY(mwc::launch_v3_pack(half, B_ssm, C_ssm, bcp, s, st));
         MWC_HIP_TRY(mwc::launch_v3_fwd(half, u, delta, A, bcp, D_ssm, h_prev, out, h_last, ckpt, s, st));
@@ -244,7 +258,7 @@ int mwc_ssm_fwd_ex(int dtype, const void* u, const void* delta, const void* A, c
     float* car_x = (float*)((char*)workspace + need / 2);
     const mwc::FwdArgs a{u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, out, h_last, ckpt, car_h, car_x,
                          p.nseg, p.cps, p.cfold, p.ncar, mwc::ScanXf{delta_bias, z, delta_softplus != 0}, out_z};
-    MWC_HIP_TRY(mwc::launch_ssm_fwd(dtype, p.spl, a, s, st));
+    MWC_HIP_TRY(mwc::launch_ssm_fwd(dtype, s.nstate, p.spl, a, s, st));
     return MWC_OK;
 }
 
@@ -275,7 +289,7 @@ int mwc_ssm_bwd_ex(int dtype, const void* u, const void* delta, const void* A, c
     if (ddelta_bias != nullptr && delta_bias == nullptr)
         return fail(MWC_ERR_INVALID_ARGUMENT, "ddelta_bias needs delta_bias");
     const bool xf = delta_bias != nullptr || delta_softplus != 0 || z != nullptr;
-    const mwc::SsmShape s{batch, seqlen, dim};
+    const mwc::SsmShape s{batch, seqlen, dim, (int)dstate};
     const size_t need = mwc::bwd_workspace_bytes(s);
     if (workspace == nullptr || workspace_bytes < need)
         return fail(MWC_ERR_WORKSPACE, "backward workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
@@ -283,8 +297,8 @@ int mwc_ssm_bwd_ex(int dtype, const void* u, const void* delta, const void* A, c
     hipStream_t st = (hipStream_t)stream;
     char* w = (char*)workspace;
     if (mwc::impl_choice() == 3) {
-        if (xf || dtype == MWC_DTYPE_BF16)
-            return fail(MWC_ERR_UNSUPPORTED, "delta_bias, delta_softplus, z and bf16 need the default kernels");
+        if (xf || dtype == MWC_DTYPE_BF16 || dstate != 16)
+            return fail(MWC_ERR_UNSUPPORTED, "delta_bias, delta_softplus, z, bf16 and N != 16 need the default kernels");
         const int ngrp = mwc::v3_groups(s);
         float* bcp = (float*)w;
         w += mwc::v3_bcp_bytes(s);
@@ -296,16 +310,16 @@ int mwc_ssm_bwd_ex(int dtype, const void* u, const void* delta, const void* A, c
         if (seqlen > 0) MWC_HIP_TRY(mwc::launch_v3_pack(half, B_ssm, C_ssm, bcp, s, st));
         MWC_HIP_TRY(mwc::launch_v3_bwd(half, u, delta, A, bcp, D_ssm, dout, dh_last, ckpt, du, ddelta, dh_prev,
                                        dA_part, dD_part, dbc_part, s, st));
-        MWC_HIP_TRY(mwc::launch_bwd_finish(dtype, dbc_part, dA_part, dD_part, nullptr, dB, dC, dA, dD, nullptr, ngrp,
+        MWC_HIP_TRY(mwc::launch_bwd_finish(dtype, 16, dbc_part, dA_part, dD_part, nullptr, dB, dC, dA, dD, nullptr, ngrp,
                                            (int)batch, s, st));
         return MWC_OK;
     }
     const mwc::SegPlan p = mwc::plan_bwd(s);
-    const int ngrp = mwc::bwd_groups(s, p.spl);
+    const int ngrp = mwc::bwd_groups(s, s.nstate, p.spl);
     float* dbc_part = (float*)w;
-    w += align256((size_t)ngrp * batch * seqlen * 32 * sizeof(float));
+    w += align256((size_t)ngrp * batch * seqlen * 2 * dstate * sizeof(float));
     float* dA_part = (float*)w;
-    w += align256((size_t)p.nseg * batch * dim * mwc::kNState * sizeof(float));
+    w += align256((size_t)p.nseg * batch * dim * dstate * sizeof(float));
     float* dD_part = (float*)w;
     w += align256((size_t)p.nseg * batch * dim * sizeof(float));
     float* dbias_part = (float*)w;
@@ -316,8 +330,8 @@ int mwc_ssm_bwd_ex(int dtype, const void* u, const void* delta, const void* A, c
     const mwc::BwdArgs a{u, delta, A, B_ssm, C_ssm, D_ssm, dout, dh_last, ckpt, du, ddelta, dh_prev,
                          dA_part, dD_part, dbc_part, car_g, car_x, p.nseg, p.cps, p.cfold, p.ncar,
                          mwc::ScanXf{delta_bias, z, delta_softplus != 0}, out, dz, dbias_part};
-    MWC_HIP_TRY(mwc::launch_ssm_bwd(dtype, p.spl, a, s, st));
-    MWC_HIP_TRY(mwc::launch_bwd_finish(dtype, dbc_part, dA_part, dD_part, dbias_part, dB, dC, dA, dD,
+    MWC_HIP_TRY(mwc::launch_ssm_bwd(dtype, s.nstate, p.spl, a, s, st));
+    MWC_HIP_TRY(mwc::launch_bwd_finish(dtype, s.nstate, dbc_part, dA_part, dD_part, dbias_part, dB, dC, dA, dD,
                                        delta_bias != nullptr ? ddelta_bias : nullptr, ngrp, p.nseg * (int)batch, s,
                                        st));
     return MWC_OK;
@@ -347,7 +361,7 @@ int mwc_ssm_step(int dtype, const void* u, const void* delta, const void* A, con
     for (const void* p : {A, B_ssm, C_ssm, h, static_cast<const void*>(h_new)})
         if ((uintptr_t)p % align != 0)
             return fail(MWC_ERR_INVALID_ARGUMENT, "A, B_ssm, C_ssm, h and h_new must be aligned to 4 elements");
-    MWC_HIP_TRY(mwc::launch_ssm_step(dtype, u, delta, A, B_ssm, C_ssm, D_ssm, h,
+    MWC_HIP_TRY(mwc::launch_ssm_step(dtype, (int)dstate, u, delta, A, B_ssm, C_ssm, D_ssm, h,
                                      mwc::ScanXf{delta_bias, z, delta_softplus != 0}, out, out_z, h_new, batch, dim,
                                      (hipStream_t)stream));
     return MWC_OK;

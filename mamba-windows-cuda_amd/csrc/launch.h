@@ -7,7 +7,13 @@ namespace mwc {
 
 struct SsmShape {
     int64_t batch, seqlen, dim;
+    int nstate = 16;  // N: 8, 16, 32 or 64
 };
+
+// The (state count NS, states per lane SPL) pairs the lane-group kernels are built for: NS/SPL lanes
+// per channel, a power of two from 4 to 16 (the DPP reductions stay inside a 16-lane row).
+#define MWC_FOR_EACH_LANE_GROUP(X) X(8, 1) X(8, 2) X(16, 1) X(16, 2) X(16, 4) X(32, 2) X(32, 4) X(64, 4)
+bool lane_group_supported(int ns, int spl);
 
 // Waves per SIMD the lane-group kernels are compiled to fit (each lane then has 512/W VGPRs).
 constexpr int fwd_min_waves(int spl) { return spl == 4 ? 1 : 3; }
@@ -25,7 +31,7 @@ SegPlan plan_bwd(const SsmShape& s);
 // Workspace carve-up (bytes, 256-aligned pieces).
 size_t fwd_workspace_bytes(const SsmShape& s);
 size_t bwd_workspace_bytes(const SsmShape& s);
-int bwd_groups(const SsmShape& s, int spl);  // channel groups that write dB/dC partials
+int bwd_groups(const SsmShape& s, int ns, int spl);  // channel groups that write dB/dC partials
 
 // Optional elementwise transforms fused around the scan (all NULL / 0: the plain scan).
 //   delta' = softplus(delta + delta_bias) (bias and softplus each optional; rows past L stay 0)
@@ -62,16 +68,16 @@ struct BwdArgs {
 };
 
 // Kernel launchers; `dt` is the storage dtype (mwc_dtype). They only enqueue work.
-hipError_t launch_ssm_fwd(int dt, int spl, const FwdArgs& a, const SsmShape& s, hipStream_t st);
-hipError_t launch_ssm_bwd(int dt, int spl, const BwdArgs& a, const SsmShape& s, hipStream_t st);
+hipError_t launch_ssm_fwd(int dt, int ns, int spl, const FwdArgs& a, const SsmShape& s, hipStream_t st);
+hipError_t launch_ssm_bwd(int dt, int ns, int spl, const BwdArgs& a, const SsmShape& s, hipStream_t st);
 // Sums the dB/dC partials of `ngroups` channel groups and the dA/dD (and, when dbias is not NULL,
 // delta_bias) partials of `nrows` rows.
-hipError_t launch_bwd_finish(int dt, const float* dbc_part, const float* dA_part,
+hipError_t launch_bwd_finish(int dt, int ns, const float* dbc_part, const float* dA_part,
                              const float* dD_part, const float* dbias_part, void* dB, void* dC, void* dA,
                              void* dD, void* dbias, int ngroups, int nrows, const SsmShape& s, hipStream_t st);
 
-// One decode step (ssm_step.hip): u, delta, z, y, y_z (batch, dim); B, C (batch, 16); h (batch, dim, 16).
-hipError_t launch_ssm_step(int dt, const void* u, const void* delta, const void* A, const void* B,
+// One decode step (ssm_step.hip): u, delta, z, y, y_z (batch, dim); B, C (batch, ns); h (batch, dim, ns).
+hipError_t launch_ssm_step(int dt, int ns, const void* u, const void* delta, const void* A, const void* B,
                            const void* C, const void* Dv, const void* h_in, const ScanXf& xf, void* y, void* y_z,
                            void* h_out, int64_t batch, int64_t dim, hipStream_t st);
 

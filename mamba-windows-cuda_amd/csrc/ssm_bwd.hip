@@ -94,22 +94,24 @@ __device__ __forceinline__ void wave_lds_fence() {
 // car_g = the reverse sweep of g -> dA_t * (g + dout_t * C_t) over the carry
 // segment from g = 0, car_x = its summed base-2 decay exponents (so it maps an
 // adjoint g arriving from its right to 2^car_x * g + car_g).
-template <typename T, int SPL, bool XF>
+template <typename T, int NS, int SPL, bool XF>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fwd_min_waves(SPL), 8)))
 ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const T* __restrict__ Cm,
                      const T* __restrict__ dout, float* __restrict__ car_g, float* __restrict__ car_x, int Bsz,
                      int L, int D, int nck, int nblk_d, int ncar, int first, int cps, ScanXf xf) {
-    constexpr int LPC = kNState / SPL;
+    constexpr int LPC = NS / SPL;
     constexpr int CPW = 64 / LPC;
     constexpr int CPB = CPW * 4;
     constexpr int TC = kCkptSteps;
     constexpr int RS = TC + 4;
     constexpr int NSG = 256 / CPB;
     constexpr int SPG = TC / NSG;
-    static_assert(NSG * SPG == TC, "tiling");
+    constexpr int BCN = TC * NS;                       // C values per chunk
+    constexpr int BCPT = BCN >= 256 ? BCN / 256 : 1;   // of them per loader thread
+    static_assert(NSG * SPG == TC && (BCN < 256 || BCN % 256 == 0), "tiling");
 
     __shared__ float s_in[2][2][CPB][RS];  // [buf][delta, dout][channel][step]
-    __shared__ float s_c[2][TC][kNState];
+    __shared__ float s_c[2][TC][NS];
 
     const int tid = threadIdx.x;
     const int lid = xcd_remap(blockIdx.x, gridDim.x);
@@ -128,14 +130,13 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
     const int lc = tid % CPB, sg = tid / CPB;
     const bool lvalid = d0 + lc < D;
     const int ld_d = lvalid ? d0 + lc : D - 1;
-    const int bc_t = tid >> 4, bc_n = tid & 15;
     const int64_t row0 = (int64_t)b * L;
 
     float A2[SPL], gc[SPL], xs[SPL];
     float amax2 = 0.f;
 #pragma unroll
     for (int j = 0; j < SPL; ++j) {
-        A2[j] = ld(A + (int64_t)d * kNState + n0 + j) * kLog2e;
+        A2[j] = ld(A + (int64_t)d * NS + n0 + j) * kLog2e;
         amax2 = __builtin_fmaxf(amax2, __builtin_fabsf(A2[j]));
         gc[j] = 0.f;
         xs[j] = 0.f;
@@ -147,7 +148,7 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
     const T* zb = XF && xf.z ? static_cast<const T*>(xf.z) : nullptr;
     const bool xform = XF && (xf.delta_bias != nullptr || xf.softplus);
     const float lbias = XF && xf.delta_bias ? ld(static_cast<const T*>(xf.delta_bias) + ld_d) : 0.f;
-    T pd[SPG], py[SPG], pz[SPG], pc;
+    T pd[SPG], py[SPG], pz[SPG], pc[BCPT];
     auto issue = [&](int k) {
         const int64_t ck = (int64_t)k * TC;
         const uint32_t rows = (uint32_t)min(TC, L - k * TC);
@@ -163,7 +164,9 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
 #pragma unroll
             for (int s = 0; s < SPG; ++s) pz[s] = buf_raw<T>(rz, lofs + s * row_bytes);
         }
-        pc = buf_raw<T>(make_rsrc(Cm + (row0 + ck) * kNState, rows * kNState * sizeof(T)), tid * sizeof(T));
+        const rsrc_t rc = make_rsrc(Cm + (row0 + ck) * NS, rows * NS * sizeof(T));
+#pragma unroll
+        for (int q = 0; q < BCPT; ++q) pc[q] = buf_raw<T>(rc, (tid * BCPT + q) * sizeof(T));
     };
     auto commit = [&](int k, int buf) {
         float vd[SPG], vy[SPG];
@@ -185,7 +188,11 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
         }
         stv<SPG>(&s_in[buf][0][lc][sg * SPG], vd);
         stv<SPG>(&s_in[buf][1][lc][sg * SPG], vy);
-        s_c[buf][bc_t][bc_n] = static_cast<float>(pc);
+#pragma unroll
+        for (int q = 0; q < BCPT; ++q) {
+            const int e = tid * BCPT + q;
+            if (BCN >= 256 || e < BCN) s_c[buf][e / NS][e % NS] = static_cast<float>(pc[q]);
+        }
     };
 
     if (k0 < k1) {
@@ -235,7 +242,7 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
         __syncthreads();
     }
     if (valid) {
-        const int64_t o = (((int64_t)b * ncar + seg) * D + d) * kNState + n0;
+        const int64_t o = (((int64_t)b * ncar + seg) * D + d) * NS + n0;
         stv<SPL>(car_g + o, gc);
         stv<SPL>(car_x + o, xs);
     }
@@ -243,7 +250,7 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
 
 // XF: the elementwise transforms of ScanXf are compiled in (the plain scan does not carry their
 // registers).
-template <typename T, int SPL, bool XF>
+template <typename T, int NS, int SPL, bool XF>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_min_waves(SPL), 8)))
 ssm_bwd_kernel(
     const T* __restrict__ u, const T* __restrict__ delta, const T* __restrict__ A, const T* __restrict__ Bm,
@@ -253,7 +260,7 @@ ssm_bwd_kernel(
     const float* __restrict__ car_g, const float* __restrict__ car_x, int Bsz, int L, int D, int nck, int nblk_d,
     int nseg, int cps, int ncar, int cfold, ScanXf xf, const T* __restrict__ yb_out, T* __restrict__ dz,
     float* __restrict__ dbias_part) {
-    constexpr int LPC = kNState / SPL;
+    constexpr int LPC = NS / SPL;
     constexpr int CPW = 64 / LPC;
     constexpr int CPB = CPW * 4;
     constexpr int TC = kCkptSteps;
@@ -261,20 +268,27 @@ ssm_bwd_kernel(
     constexpr int NSG = 256 / CPB;
     constexpr int SPG = TC / NSG;
     constexpr int OS = CPB + 4;
-    constexpr int HALF = CPW / 2;  // channels each folding lane sums
-    static_assert(NSG * SPG == TC && CPW >= 2, "tiling");
+    constexpr int BCN = TC * NS;                       // B (and C) values per chunk
+    constexpr int BCPT = BCN >= 256 ? BCN / 256 : 1;   // of them per loader thread
+    // fold: each 4-step phase produces 2*NS values (dB, dC) per slot, NQ groups of 4 per slot; the
+    // 16 lanes of a slot take NQ groups, LPI lanes per group splitting the channels (or, past 16
+    // groups, QPL groups per lane)
+    constexpr int NQ = NS / 2;
+    constexpr int LPI = NQ <= 16 ? 16 / NQ : 1;
+    constexpr int QPL = NQ <= 16 ? 1 : NQ / 16;
+    static_assert(NSG * SPG == TC && CPW >= LPI && (BCN < 256 || BCN % 256 == 0) && LPI <= 4, "tiling");
 
     // [delta, delta*u, u, dout] planes of [channel][step]; planes are AS floats apart
     // (AS = 16 mod 64 banks) so the delta*u and dout weights of one channel sit in different banks
     constexpr int AS = CPB * RS + 16;
     __shared__ float s_in_raw[4 * AS];
-    __shared__ float s_bc[TC][2 * kNState];
+    __shared__ float s_bc[TC][2 * NS];
     // wave-private slabs of g_t (plane 0) and h_t (plane 1): [wave][plane][slot][channel][16];
     // a 16-lane group deposits 64 consecutive floats, plane 1 is offset by 32 banks
-    constexpr int PL = kRedSlots * CPW * kNState + 32;
+    constexpr int PL = kRedSlots * CPW * NS + 32;
     __shared__ float s_red[4][2 * PL];
     auto s_in = [&](int plane, int ch) -> float* { return &s_in_raw[plane * AS + ch * RS]; };
-    __shared__ float s_part[4][TC][2 * kNState];
+    __shared__ float s_part[4][TC][2 * NS];
     __shared__ float s_out[2][TC][OS];  // [du, ddelta][step][channel]
     __shared__ int s_flag;              // index of the last staged chunk that needs the exponent clamp
 
@@ -299,22 +313,22 @@ ssm_bwd_kernel(
     const int lc = tid % CPB, sg = tid / CPB;
     const bool lvalid = d0 + lc < D;
     const int ld_d = lvalid ? d0 + lc : D - 1;
-    const int bc_t = tid >> 4, bc_n = tid & 15;
     const int64_t row0 = (int64_t)b * L;
 
-    // folding roles: slot rs (step i+rs), value quad q (dB n=4q.. for q<4, dC for q>=4), channel half
-    const int rs = lane >> 4, rq = (lane >> 1) & 7, rhalf = lane & 1;
+    // folding roles: slot rs (step i+rs), first value group rq0 (groups < NQ/2 are dB n = 4*group..,
+    // the rest dC), channel subset rsub of the group's LPI lanes
+    const int rs = lane >> 4, rq0 = ((lane & 15) / LPI) * QPL, rsub = (lane & 15) % LPI;
 
     float A2[SPL], An[SPL], gc[SPL], dAacc[SPL];
 #pragma unroll
     for (int j = 0; j < SPL; ++j) {
-        An[j] = ld(A + (int64_t)d * kNState + n0 + j);
+        An[j] = ld(A + (int64_t)d * NS + n0 + j);
         A2[j] = An[j] * kLog2e;
-        gc[j] = dh_last != nullptr ? ld(dh_last + ((int64_t)b * D + d) * kNState + n0 + j) : 0.f;
+        gc[j] = dh_last != nullptr ? ld(dh_last + ((int64_t)b * D + d) * NS + n0 + j) : 0.f;
         dAacc[j] = 0.f;
     }
     for (int j = ncar - 1; j >= seg * cfold; --j) {  // g -> 2^xsum * g + G of each following carry segment
-        const int64_t o = (((int64_t)b * ncar + j) * D + d) * kNState + n0;
+        const int64_t o = (((int64_t)b * ncar + j) * D + d) * NS + n0;
         float cg[SPL], cx[SPL];
         ldv<SPL>(car_g + o, cg);
         ldv<SPL>(car_x + o, cx);
@@ -323,7 +337,7 @@ ssm_bwd_kernel(
     }
     float dDacc = 0.f;
     const float Dd = ld(Dv + d);
-    const float* ckb = ckpt + ((int64_t)b * nck * D + d) * kNState + n0;
+    const float* ckb = ckpt + ((int64_t)b * nck * D + d) * NS + n0;
 
     // Chunk k's rows are read through buffer resources spanning exactly its min(16, L - 16k) rows:
     // rows past L and channels past D (offset kOob) read as 0 and their stores are dropped.
@@ -333,7 +347,7 @@ ssm_bwd_kernel(
     const int64_t rowD = row0 * D;
     const T* zb = XF && xf.z ? static_cast<const T*>(xf.z) : nullptr;
     const bool xform = XF && (xf.delta_bias != nullptr || xf.softplus);
-    T pu[SPG], pd[SPG], py[SPG], pz[SPG], pyo[SPG], pb, pc;
+    T pu[SPG], pd[SPG], py[SPG], pz[SPG], pyo[SPG], pb[BCPT], pc[BCPT];
     float hnext[SPL];
     auto issue = [&](int k) {
         const int64_t ck = (int64_t)k * TC;
@@ -356,14 +370,19 @@ ssm_bwd_kernel(
                 pyo[s] = buf_raw<T>(ro, lofs + s * row_bytes);
             }
         }
-        const uint32_t bc_bytes = rows * kNState * sizeof(T);
-        pb = buf_raw<T>(make_rsrc(Bm + (row0 + ck) * kNState, bc_bytes), tid * sizeof(T));
-        pc = buf_raw<T>(make_rsrc(Cm + (row0 + ck) * kNState, bc_bytes), tid * sizeof(T));
-        ldv<SPL>(ckb + (int64_t)k * D * kNState, hnext);
+        const uint32_t bc_bytes = rows * NS * sizeof(T);
+        const rsrc_t rb = make_rsrc(Bm + (row0 + ck) * NS, bc_bytes);
+        const rsrc_t rc = make_rsrc(Cm + (row0 + ck) * NS, bc_bytes);
+#pragma unroll
+        for (int q = 0; q < BCPT; ++q) {  // value e = tid*BCPT + q of the chunk's (step, n) rows
+            pb[q] = buf_raw<T>(rb, (tid * BCPT + q) * sizeof(T));
+            pc[q] = buf_raw<T>(rc, (tid * BCPT + q) * sizeof(T));
+        }
+        ldv<SPL>(ckb + (int64_t)k * D * NS, hnext);
     };
     float lamax2 = 0.f;  // max_n |A[ld_d][n]| * log2(e): the loader flags chunks that reach the clamp
 #pragma unroll
-    for (int n = 0; n < kNState; ++n) lamax2 = __builtin_fmaxf(lamax2, __builtin_fabsf(ld(A + (int64_t)ld_d * kNState + n)));
+    for (int n = 0; n < NS; ++n) lamax2 = __builtin_fmaxf(lamax2, __builtin_fabsf(ld(A + (int64_t)ld_d * NS + n)));
     lamax2 *= kLog2e;
     const float lbias = XF && xf.delta_bias ? ld(static_cast<const T*>(xf.delta_bias) + ld_d) : 0.f;
     // d delta / d delta' (softplus) of the loader's elements, for the chunk being stored and the next
@@ -410,8 +429,14 @@ ssm_bwd_kernel(
         stv<SPG>((s_in(1, lc) + sg * SPG), vdu);
         stv<SPG>((s_in(2, lc) + sg * SPG), vu);
         stv<SPG>((s_in(3, lc) + sg * SPG), vy);
-        s_bc[bc_t][bc_n] = static_cast<float>(pb);
-        s_bc[bc_t][kNState + bc_n] = static_cast<float>(pc);
+#pragma unroll
+        for (int q = 0; q < BCPT; ++q) {
+            const int e = tid * BCPT + q;
+            if (BCN >= 256 || e < BCN) {
+                s_bc[e / NS][e % NS] = static_cast<float>(pb[q]);
+                s_bc[e / NS][NS + e % NS] = static_cast<float>(pc[q]);
+            }
+        }
     };
 
     float hin[SPL];
@@ -478,23 +503,30 @@ ssm_bwd_kernel(
         // B/C are read one step ahead and u/dout one 4-step group ahead of use; every 4 steps the
         // wave folds the phase's deposits over its channels.
         auto fold = [&](int phase) {
-            const bool is_c = rq >= 4;
-            const float* plane = is_c ? red_h : red_g;
-            const float* wrow = s_in(is_c ? 3 : 1, wave * CPW) + phase * kRedSlots + rs;
-            const int q4 = (rq & 3) * 4;
-            float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int m = 0; m < HALF; ++m) {
-                const int ch = 2 * m + rhalf;  // the two lanes of a pair take alternate channels
-                float v4[4];
-                ldv<4>(plane + (rs * CPW + ch) * kNState + q4, v4);
-                const float wgt = wrow[ch * RS];
+            for (int qq = 0; qq < QPL; ++qq) {
+                const int rq = rq0 + qq;
+                const bool is_c = rq >= NQ / 2;
+                const float* plane = is_c ? red_h : red_g;
+                const float* wrow = s_in(is_c ? 3 : 1, wave * CPW) + phase * kRedSlots + rs;
+                const int q4 = (rq % (NQ / 2)) * 4;
+                float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int q = 0; q < 4; ++q) acc[q] = __builtin_fmaf(v4[q], wgt, acc[q]);
+                for (int m = 0; m < CPW / LPI; ++m) {
+                    const int ch = LPI * m + rsub;  // the LPI lanes of a group take interleaved channels
+                    float v4[4];
+                    ldv<4>(plane + (rs * CPW + ch) * NS + q4, v4);
+                    const float wgt = wrow[ch * RS];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) acc[q] = __builtin_fmaf(v4[q], wgt, acc[q]);
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    if constexpr (LPI >= 2) acc[q] += dpp<kDppXor1>(acc[q]);
+                    if constexpr (LPI >= 4) acc[q] += dpp<kDppXor2>(acc[q]);
+                }
+                if (rsub == 0) stv<4>(&s_part[wave][phase * kRedSlots + rs][rq * 4], acc);
             }
-#pragma unroll
-            for (int q = 0; q < 4; ++q) acc[q] += dpp<kDppXor1>(acc[q]);
-            if (rhalf == 0) stv<4>(&s_part[wave][phase * kRedSlots + rs][rq * 4], acc);
         };
         {
             float uq[4], yq[4], dq[4], uqn[4], yqn[4], dqn[4], Bn[SPL], Cn[SPL];
@@ -502,7 +534,7 @@ ssm_bwd_kernel(
             ldv<4>(s_in(3, c) + TC - 4, yqn);
             ldv<4>(s_in(0, c) + TC - 4, dqn);
             ldv<SPL>(&s_bc[TC - 1][n0], Bn);
-            ldv<SPL>(&s_bc[TC - 1][kNState + n0], Cn);
+            ldv<SPL>(&s_bc[TC - 1][NS + n0], Cn);
 #pragma unroll
             for (int i = TC - 1; i >= 0; --i) {
                 const int slot = i % kRedSlots, phase = i / kRedSlots;
@@ -527,7 +559,7 @@ ssm_bwd_kernel(
                 }
                 if (i > 0) {
                     ldv<SPL>(&s_bc[i > 0 ? i - 1 : 0][n0], Bn);
-                    ldv<SPL>(&s_bc[i > 0 ? i - 1 : 0][kNState + n0], Cn);
+                    ldv<SPL>(&s_bc[i > 0 ? i - 1 : 0][NS + n0], Cn);
                 }
                 // keep the next step's operand reads here, a full step ahead of their use (the
                 // scheduler would otherwise sink them next to the use and expose the LDS latency)
@@ -552,8 +584,8 @@ ssm_bwd_kernel(
                 s_out[1][i][c] = __builtin_fmaf(ui, r1, r2);
                 dDacc = __builtin_fmaf(yo, ui, dDacc);
                 const int sl = slot * CPW + cw;
-                stv<SPL>(red_g + sl * kNState + n0, gt);
-                stv<SPL>(red_h + sl * kNState + n0, H[i]);
+                stv<SPL>(red_g + sl * NS + n0, gt);
+                stv<SPL>(red_h + sl * NS + n0, H[i]);
                 if (slot == 0) {
                     wave_lds_fence();
                     fold(phase);
@@ -583,10 +615,10 @@ ssm_bwd_kernel(
             }
         }
         // this workgroup's dB/dC partial for the chunk (sum of its 4 waves)
-        for (int o = tid; o < TC * 2 * kNState; o += 256) {
-            const int tt = o >> 5, v = o & 31;
+        for (int o = tid; o < TC * 2 * NS; o += 256) {
+            const int tt = o / (2 * NS), v = o % (2 * NS);
             const float s = s_part[0][tt][v] + s_part[1][tt][v] + s_part[2][tt][v] + s_part[3][tt][v];
-            if (t0 + tt < L) dbc_part[(((int64_t)blk * Bsz + b) * L + t0 + tt) * 32 + v] = s;
+            if (t0 + tt < L) dbc_part[(((int64_t)blk * Bsz + b) * L + t0 + tt) * (2 * NS) + v] = s;
         }
         __syncthreads();  // the next chunk's tile is staged; s_out / s_part are free again
     }
@@ -594,10 +626,10 @@ ssm_bwd_kernel(
     if (valid) {
         if (dh_prev != nullptr && seg == 0) {
 #pragma unroll
-            for (int j = 0; j < SPL; ++j) st(dh_prev + ((int64_t)b * D + d) * kNState + n0 + j, gc[j]);
+            for (int j = 0; j < SPL; ++j) st(dh_prev + ((int64_t)b * D + d) * NS + n0 + j, gc[j]);
         }
         const int64_t pr = (int64_t)seg * Bsz + b;  // partial row
-        stv<SPL>(dA_part + (pr * D + d) * kNState + n0, dAacc);
+        stv<SPL>(dA_part + (pr * D + d) * NS + n0, dAacc);
         if (g == 0) dD_part[pr * D + d] = dDacc;
     }
     if constexpr (XF) {
@@ -618,7 +650,7 @@ ssm_bwd_kernel(
 // The backward's reductions, one launch: blocks [0, nblk_bc) sum the channel-group dB/dC partials
 // (4 consecutive values per thread, groups in order), the rest sum the (segment, batch) dA/dD
 // partials in order. Fixed summation orders: the results are deterministic.
-template <typename T>
+template <typename T, int NS>
 __global__ void __launch_bounds__(256) bwd_finish_kernel(const float* __restrict__ part, T* __restrict__ dB,
                                                          T* __restrict__ dC, int ngrp, int64_t rows, int nblk_bc,
                                                          const float* __restrict__ dA_part,
@@ -626,9 +658,9 @@ __global__ void __launch_bounds__(256) bwd_finish_kernel(const float* __restrict
                                                          T* __restrict__ dD, int nrows, int D,
                                                          const float* __restrict__ dbias_part, T* __restrict__ dbias) {
     if ((int)blockIdx.x < nblk_bc) {
-        const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;  // over rows*32, 4-aligned
-        if (i >= rows * 32) return;
-        const int64_t stride = rows * 32;
+        const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;  // over rows*2NS, 4-aligned
+        if (i >= rows * 2 * NS) return;
+        const int64_t stride = rows * 2 * NS;
         const float* p = part + i;
         float acc[4] = {0.f, 0.f, 0.f, 0.f};
         int q = 0;
@@ -651,15 +683,15 @@ __global__ void __launch_bounds__(256) bwd_finish_kernel(const float* __restrict
             acc[2] += v.z;
             acc[3] += v.w;
         }
-        const int64_t r = i >> 5;
-        const int col = (int)(i & 31);  // the 4 values are all dB (col < 16) or all dC
-        T* dst = col < kNState ? dB + r * kNState + col : dC + r * kNState + col - kNState;
+        const int64_t r = i / (2 * NS);
+        const int col = (int)(i % (2 * NS));  // the 4 values are all dB (col < NS) or all dC
+        T* dst = col < NS ? dB + r * NS + col : dC + r * NS + col - NS;
 #pragma unroll
         for (int u = 0; u < 4; ++u) st(dst + u, acc[u]);
         return;
     }
     const int64_t i = (int64_t)(blockIdx.x - nblk_bc) * 256 + threadIdx.x;
-    const int64_t nA = (int64_t)D * kNState;
+    const int64_t nA = (int64_t)D * NS;
     if (i < nA) {
         float s = 0.f;
         for (int r = 0; r < nrows; ++r) s += dA_part[(int64_t)r * nA + i];
@@ -677,22 +709,22 @@ __global__ void __launch_bounds__(256) bwd_finish_kernel(const float* __restrict
     }
 }
 
-int bwd_groups(const SsmShape& s, int spl) {
-    const int cpb = 4 * 64 / (kNState / spl);
+int bwd_groups(const SsmShape& s, int ns, int spl) {
+    const int cpb = 4 * 64 / (ns / spl);
     return (int)((s.dim + cpb - 1) / cpb);
 }
 
-template <typename T, int SPL, bool XF>
+template <typename T, int NS, int SPL, bool XF>
 static hipError_t bwd_inst(const BwdArgs& a, const SsmShape& s, hipStream_t st) {
-    const int nblk_d = bwd_groups(s, SPL);
+    const int nblk_d = bwd_groups(s, NS, SPL);
     const int nck = (int)((s.seqlen + kCkptSteps - 1) / kCkptSteps);
     const int per_seg = nblk_d * (int)s.batch;
     if (a.nseg > 1)  // carries of every chunk after the first segment
-        hipLaunchKernelGGL((ssm_bwd_carry_kernel<T, SPL, XF>), dim3(per_seg * a.ncar), dim3(256), 0, st,
+        hipLaunchKernelGGL((ssm_bwd_carry_kernel<T, NS, SPL, XF>), dim3(per_seg * a.ncar), dim3(256), 0, st,
                            (const T*)a.delta, (const T*)a.A, (const T*)a.C, (const T*)a.dout, a.car_g, a.car_x,
                            (int)s.batch, (int)s.seqlen, (int)s.dim, nck, nblk_d, a.ncar, a.cps, a.cps / a.cfold,
                            a.xf);
-    hipLaunchKernelGGL((ssm_bwd_kernel<T, SPL, XF>), dim3(per_seg * a.nseg), dim3(256), 0, st, (const T*)a.u,
+    hipLaunchKernelGGL((ssm_bwd_kernel<T, NS, SPL, XF>), dim3(per_seg * a.nseg), dim3(256), 0, st, (const T*)a.u,
                        (const T*)a.delta, (const T*)a.A, (const T*)a.B, (const T*)a.C, (const T*)a.Dv,
                        (const T*)a.dout, (const T*)a.dh_last, a.ckpt, (T*)a.du, (T*)a.ddelta, (T*)a.dh_prev,
                        a.dA_part, a.dD_part, a.dbc_part, a.car_g, a.car_x, (int)s.batch, (int)s.seqlen, (int)s.dim,
@@ -700,42 +732,48 @@ static hipError_t bwd_inst(const BwdArgs& a, const SsmShape& s, hipStream_t st) 
     return hipGetLastError();
 }
 
-template <typename T, int SPL>
+template <typename T, int NS, int SPL>
 static hipError_t bwd_inst(const BwdArgs& a, const SsmShape& s, hipStream_t st) {
     const bool xf = a.xf.delta_bias != nullptr || a.xf.softplus || a.xf.z != nullptr;
-    return xf ? bwd_inst<T, SPL, true>(a, s, st) : bwd_inst<T, SPL, false>(a, s, st);
+    return xf ? bwd_inst<T, NS, SPL, true>(a, s, st) : bwd_inst<T, NS, SPL, false>(a, s, st);
 }
 
-hipError_t launch_ssm_bwd(int dt, int spl, const BwdArgs& a, const SsmShape& s, hipStream_t st) {
-#define MWC_BWD_SPL(S) \
-    if (spl == S) MWC_DISPATCH_DTYPE(dt, TT, return bwd_inst<TT, S>(a, s, st));
-    MWC_BWD_SPL(1)
-    MWC_BWD_SPL(2)
-    MWC_BWD_SPL(4)
-#undef MWC_BWD_SPL
+hipError_t launch_ssm_bwd(int dt, int ns, int spl, const BwdArgs& a, const SsmShape& s, hipStream_t st) {
+#define MWC_BWD(N, S) \
+    if (ns == N && spl == S) MWC_DISPATCH_DTYPE(dt, TT, return bwd_inst<TT, N, S>(a, s, st));
+    MWC_FOR_EACH_LANE_GROUP(MWC_BWD)
+#undef MWC_BWD
     return hipErrorInvalidValue;
 }
 
-template <typename T>
+template <typename T, int NS>
 static hipError_t finish_t(const float* dbc_part, const float* dA_part, const float* dD_part,
                            const float* dbias_part, void* dB, void* dC, void* dA, void* dD, void* dbias, int ngrp,
                            int nrows, const SsmShape& s, hipStream_t st) {
     const int64_t rows = s.batch * s.seqlen;
-    const int nblk_bc = (int)((rows * 32 / 4 + 255) / 256);
-    const int64_t n2 = s.dim * kNState + 2 * s.dim;
+    const int nblk_bc = (int)((rows * 2 * NS / 4 + 255) / 256);
+    const int64_t n2 = s.dim * NS + 2 * s.dim;
     const int nblk_ad = (int)((n2 + 255) / 256);
-    hipLaunchKernelGGL(bwd_finish_kernel<T>, dim3(nblk_bc + nblk_ad), dim3(256), 0, st, dbc_part, (T*)dB, (T*)dC,
-                       ngrp, rows, nblk_bc, dA_part, dD_part, (T*)dA, (T*)dD, nrows, (int)s.dim, dbias_part,
+    hipLaunchKernelGGL((bwd_finish_kernel<T, NS>), dim3(nblk_bc + nblk_ad), dim3(256), 0, st, dbc_part, (T*)dB,
+                       (T*)dC, ngrp, rows, nblk_bc, dA_part, dD_part, (T*)dA, (T*)dD, nrows, (int)s.dim, dbias_part,
                        (T*)dbias);
     return hipGetLastError();
 }
 
-hipError_t launch_bwd_finish(int dt, const float* dbc_part, const float* dA_part, const float* dD_part,
+hipError_t launch_bwd_finish(int dt, int ns, const float* dbc_part, const float* dA_part, const float* dD_part,
                              const float* dbias_part, void* dB, void* dC, void* dA, void* dD, void* dbias,
                              int ngroups, int nrows, const SsmShape& s, hipStream_t st) {
-    MWC_DISPATCH_DTYPE(dt, TT,
-                       return finish_t<TT>(dbc_part, dA_part, dD_part, dbias_part, dB, dC, dA, dD, dbias, ngroups,
-                                           nrows, s, st));
+#define MWC_FIN(N)                                                                                              \
+    if (ns == N)                                                                                                \
+        MWC_DISPATCH_DTYPE(dt, TT,                                                                              \
+                           return finish_t<TT, N>(dbc_part, dA_part, dD_part, dbias_part, dB, dC, dA, dD, dbias, \
+                                                  ngroups, nrows, s, st));
+    MWC_FIN(8)
+    MWC_FIN(16)
+    MWC_FIN(32)
+    MWC_FIN(64)
+#undef MWC_FIN
+    return hipErrorInvalidValue;
 }
 
 }  // namespace mwc

@@ -74,7 +74,7 @@ enum FwdMode { kMain = 0, kState = 1, kCarry = 2 };
 
 // XF: the elementwise transforms of ScanXf are compiled in (the plain scan does not carry their
 // registers).
-template <typename T, int SPL, int MODE, bool XF>
+template <typename T, int NS, int SPL, int MODE, bool XF>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fwd_min_waves(SPL), 8)))
 ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __restrict__ A,
                const T* __restrict__ Bm, const T* __restrict__ Cm, const T* __restrict__ Dv,
@@ -83,7 +83,7 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
                int nseg, int cps, int ncar, int cfold, ScanXf xf, T* __restrict__ out_z) {
     constexpr bool HAS_OUT = MODE == kMain;
     constexpr bool CARRY = MODE == kCarry;
-    constexpr int LPC = kNState / SPL;  // lanes per channel
+    constexpr int LPC = NS / SPL;  // lanes per channel
     constexpr int CPW = 64 / LPC;       // channels per wave
     constexpr int CPB = CPW * 4;        // channels per workgroup
     constexpr int TC = kCkptSteps;      // steps per chunk
@@ -91,10 +91,12 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
     constexpr int NSG = 256 / CPB;      // loader step groups
     constexpr int SPG = TC / NSG;       // steps per loader thread
     constexpr int YS = CPB + 4;         // LDS row stride of the output tile (16 mod 64 banks apart)
-    static_assert(NSG * SPG == TC, "loader tiling");
+    constexpr int BCN = TC * NS;                       // B (and C) values per chunk
+    constexpr int BCPT = BCN >= 256 ? BCN / 256 : 1;   // of them per loader thread
+    static_assert(NSG * SPG == TC && (BCN < 256 || BCN % 256 == 0), "loader tiling");
 
     __shared__ float s_in[2][2][CPB][RS];  // [buf][delta, delta*u][channel][step]
-    __shared__ float s_bc[2][TC][HAS_OUT ? 2 * kNState : kNState];
+    __shared__ float s_bc[2][TC][HAS_OUT ? 2 * NS : NS];
     __shared__ float s_y[HAS_OUT ? 2 : 1][HAS_OUT ? TC : 1][HAS_OUT ? YS : 1];
 
     const int tid = threadIdx.x;
@@ -118,19 +120,18 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
     const int lc = tid % CPB, sg = tid / CPB;
     const bool lvalid = d0 + lc < D;
     const int ld_d = lvalid ? d0 + lc : D - 1;
-    const int bc_t = tid >> 4, bc_n = tid & 15;
     const int64_t row0 = (int64_t)b * L;
     // carries of the ncar carry segments (cfold per main segment): car_[b][carry segment][d][n]
-    const int64_t car0 = ((int64_t)b * ncar * D + d) * kNState + n0;
-    const int64_t car_seg = (int64_t)D * kNState;
+    const int64_t car0 = ((int64_t)b * ncar * D + d) * NS + n0;
+    const int64_t car_seg = (int64_t)D * NS;
 
     float A2[SPL], h[SPL], xs[SPL];
     float amax2 = 0.f;  // max_j |A_j| * log2(e) over this lane's states
 #pragma unroll
     for (int j = 0; j < SPL; ++j) {
-        A2[j] = ld(A + (int64_t)d * kNState + n0 + j) * kLog2e;
+        A2[j] = ld(A + (int64_t)d * NS + n0 + j) * kLog2e;
         amax2 = __builtin_fmaxf(amax2, __builtin_fabsf(A2[j]));
-        h[j] = (!CARRY && h_prev) ? ld(h_prev + ((int64_t)b * D + d) * kNState + n0 + j) : 0.f;
+        h[j] = (!CARRY && h_prev) ? ld(h_prev + ((int64_t)b * D + d) * NS + n0 + j) : 0.f;
         xs[j] = 0.f;
     }
     if constexpr (!CARRY) {
@@ -146,14 +147,14 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
     // rows past L and channels past D (offset kOob) read as 0, which is the padding the scan needs.
     const T* ub = u + row0 * D;
     const T* db = delta + row0 * D;
-    const T* Bb = Bm + row0 * kNState;
-    const T* Cb = Cm + row0 * kNState;
+    const T* Bb = Bm + row0 * NS;
+    const T* Cb = Cm + row0 * NS;
     const uint32_t lofs = lvalid ? ((uint32_t)(sg * SPG) * (uint32_t)D + (uint32_t)ld_d) * sizeof(T) : kOob;
     const uint32_t row_bytes = (uint32_t)D * sizeof(T);
     auto chunk_rows = [&](int k) { return (uint32_t)min(TC, L - k * TC); };
     // z is read only when the gated output is stored
     const T* zb = XF && HAS_OUT && xf.z && out_z ? static_cast<const T*>(xf.z) + row0 * D : nullptr;
-    T pu[SPG], pd[SPG], pz[SPG], pb, pc;
+    T pu[SPG], pd[SPG], pz[SPG], pb[BCPT], pc[BCPT];
     auto issue = [&](int k) {
         const int64_t ck = (int64_t)k * TC;
         const uint32_t rows = chunk_rows(k);
@@ -169,8 +170,13 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
 #pragma unroll
             for (int s = 0; s < SPG; ++s) pz[s] = buf_raw<T>(rz, lofs + s * row_bytes);
         }
-        pb = buf_raw<T>(make_rsrc(Bb + ck * kNState, rows * kNState * sizeof(T)), tid * sizeof(T));
-        if constexpr (HAS_OUT) pc = buf_raw<T>(make_rsrc(Cb + ck * kNState, rows * kNState * sizeof(T)), tid * sizeof(T));
+        const rsrc_t rb = make_rsrc(Bb + ck * NS, rows * NS * sizeof(T));
+        const rsrc_t rc = make_rsrc(Cb + ck * NS, rows * NS * sizeof(T));
+#pragma unroll
+        for (int q = 0; q < BCPT; ++q) {  // value e = tid*BCPT + q of the chunk's (step, n) rows
+            pb[q] = buf_raw<T>(rb, (tid * BCPT + q) * sizeof(T));
+            if constexpr (HAS_OUT) pc[q] = buf_raw<T>(rc, (tid * BCPT + q) * sizeof(T));
+        }
     };
     // D*u of the loader's (channel, steps) for the chunk being computed and the next one; the
     // loader thread also stores those outputs, so the consumer lanes never touch u
@@ -199,8 +205,14 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
         }
         vst<SPG>(&s_in[buf][0][lc][sg * SPG], vd);
         vst<SPG>(&s_in[buf][1][lc][sg * SPG], vdu);
-        s_bc[buf][bc_t][bc_n] = static_cast<float>(pb);
-        if constexpr (HAS_OUT) s_bc[buf][bc_t][kNState + bc_n] = static_cast<float>(pc);
+#pragma unroll
+        for (int q = 0; q < BCPT; ++q) {
+            const int e = tid * BCPT + q;
+            if (BCN >= 256 || e < BCN) {
+                s_bc[buf][e / NS][e % NS] = static_cast<float>(pb[q]);
+                if constexpr (HAS_OUT) s_bc[buf][e / NS][NS + e % NS] = static_cast<float>(pc[q]);
+            }
+        }
     };
 
     if (k0 < k1) {  // every segment holds a chunk unless L == 0 (then h_last = h_prev)
@@ -208,7 +220,7 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
         commit(k0, k0 & 1);
     }
     __syncthreads();
-    float* ckb = (!CARRY && ckpt) ? ckpt + ((int64_t)b * nck * D + d) * kNState + n0 : nullptr;
+    float* ckb = (!CARRY && ckpt) ? ckpt + ((int64_t)b * nck * D + d) * NS + n0 : nullptr;
     T* ob = HAS_OUT && out != nullptr ? out + row0 * D : nullptr;
 
     for (int k = k0; k < k1; ++k) {
@@ -220,7 +232,7 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
             if constexpr (XF) gz_cur[s] = gz_nxt[s];
         }
         if (more) issue(k + 1);
-        if (ckb != nullptr && valid) vst<SPL>(ckb + (int64_t)k * D * kNState, h);
+        if (ckb != nullptr && valid) vst<SPL>(ckb + (int64_t)k * D * NS, h);
 
         // the whole chunk's operands, read up front so LDS latency is paid once per chunk
         float dt[TC], dtu[TC], Bv[TC][SPL], Cv[TC][SPL];
@@ -229,7 +241,7 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
 #pragma unroll
         for (int i = 0; i < TC; ++i) {
             lds_ld<SPL>(&s_bc[buf][i][n0], Bv[i]);
-            if constexpr (HAS_OUT) lds_ld<SPL>(&s_bc[buf][i][kNState + n0], Cv[i]);
+            if constexpr (HAS_OUT) lds_ld<SPL>(&s_bc[buf][i][NS + n0], Cv[i]);
         }
         // |delta*A| <= 88 for the whole chunk (the usual case) -> no clamp needed
         float dmax = 0.f;
@@ -291,46 +303,44 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
         }
     } else if (h_last != nullptr && valid && seg == nseg - 1) {
 #pragma unroll
-        for (int j = 0; j < SPL; ++j) st(h_last + ((int64_t)b * D + d) * kNState + n0 + j, h[j]);
+        for (int j = 0; j < SPL; ++j) st(h_last + ((int64_t)b * D + d) * NS + n0 + j, h[j]);
     }
 }
 
-template <typename T, int SPL, int MODE, bool XF>
+template <typename T, int NS, int SPL, int MODE, bool XF>
 static void fwd_launch(const FwdArgs& a, const SsmShape& s, int nseg_launched, hipStream_t st) {
-    constexpr int CPB = 4 * 64 / (kNState / SPL);
+    constexpr int CPB = 4 * 64 / (NS / SPL);
     const int nblk_d = (int)((s.dim + CPB - 1) / CPB);
     const int nck = (int)((s.seqlen + kCkptSteps - 1) / kCkptSteps);
     const int grid = nblk_d * (int)s.batch * nseg_launched;
-    hipLaunchKernelGGL((ssm_fwd_kernel<T, SPL, MODE, XF>), dim3(grid), dim3(256), 0, st, (const T*)a.u,
+    hipLaunchKernelGGL((ssm_fwd_kernel<T, NS, SPL, MODE, XF>), dim3(grid), dim3(256), 0, st, (const T*)a.u,
                        (const T*)a.delta, (const T*)a.A, (const T*)a.B, (const T*)a.C, (const T*)a.Dv,
                        (const T*)a.h_prev, (T*)a.out, (T*)a.h_last, a.ckpt, a.car_h, a.car_x, (int)s.batch,
                        (int)s.seqlen, (int)s.dim, nck, nblk_d, a.nseg, MODE == kCarry ? a.cps / a.cfold : a.cps,
                        a.ncar, a.cfold, a.xf, (T*)a.out_z);
 }
 
-template <typename T, int SPL, bool XF>
+template <typename T, int NS, int SPL, bool XF>
 static hipError_t fwd_inst(const FwdArgs& a, const SsmShape& s, hipStream_t st) {
-    if (a.nseg > 1) fwd_launch<T, SPL, kCarry, XF>(a, s, a.ncar, st);  // carries of all chunks before the last segment
+    if (a.nseg > 1) fwd_launch<T, NS, SPL, kCarry, XF>(a, s, a.ncar, st);  // carries of all chunks before the last segment
     if (a.out != nullptr || a.out_z != nullptr)
-        fwd_launch<T, SPL, kMain, XF>(a, s, a.nseg, st);
+        fwd_launch<T, NS, SPL, kMain, XF>(a, s, a.nseg, st);
     else
-        fwd_launch<T, SPL, kState, XF>(a, s, a.nseg, st);
+        fwd_launch<T, NS, SPL, kState, XF>(a, s, a.nseg, st);
     return hipGetLastError();
 }
 
-template <typename T, int SPL>
+template <typename T, int NS, int SPL>
 static hipError_t fwd_inst(const FwdArgs& a, const SsmShape& s, hipStream_t st) {
     const bool xf = a.xf.delta_bias != nullptr || a.xf.softplus || a.xf.z != nullptr;
-    return xf ? fwd_inst<T, SPL, true>(a, s, st) : fwd_inst<T, SPL, false>(a, s, st);
+    return xf ? fwd_inst<T, NS, SPL, true>(a, s, st) : fwd_inst<T, NS, SPL, false>(a, s, st);
 }
 
-hipError_t launch_ssm_fwd(int dt, int spl, const FwdArgs& a, const SsmShape& s, hipStream_t st) {
-#define MWC_FWD_SPL(S) \
-    if (spl == S) MWC_DISPATCH_DTYPE(dt, TT, return fwd_inst<TT, S>(a, s, st));
-    MWC_FWD_SPL(1)
-    MWC_FWD_SPL(2)
-    MWC_FWD_SPL(4)
-#undef MWC_FWD_SPL
+hipError_t launch_ssm_fwd(int dt, int ns, int spl, const FwdArgs& a, const SsmShape& s, hipStream_t st) {
+#define MWC_FWD(N, S) \
+    if (ns == N && spl == S) MWC_DISPATCH_DTYPE(dt, TT, return fwd_inst<TT, N, S>(a, s, st));
+    MWC_FOR_EACH_LANE_GROUP(MWC_FWD)
+#undef MWC_FWD
     return hipErrorInvalidValue;
 }
 

@@ -6,24 +6,24 @@
 // y_z = y * silu(z)). The state is read and written in the input dtype, (batch, dim, 16), and the
 // output state may alias the input one (in-place update).
 //
-// Mapping: 4 consecutive lanes hold one channel's 16 states, 4 per lane, so the state moves as
+// Mapping: N/4 consecutive lanes hold one channel's N states, 4 per lane, so the state moves as
 // coalesced rows of 8- or 16-byte accesses and the C-contraction is an in-lane FMA chain plus a
-// 4-lane DPP sum. The step is bound by the state's round trip through HBM (2 * batch * dim * 16 * s
-// bytes) and, at small batch, by launch latency.
+// DPP sum over the N/4 lanes. The step is bound by the state's round trip through HBM
+// (2 * batch * dim * N * s bytes) and, at small batch, by launch latency.
 #include "common.h"
 #include "launch.h"
 
 namespace mwc {
 
-constexpr int kStepSpl = 4;                    // states per lane
-constexpr int kStepLpc = kNState / kStepSpl;   // lanes per channel
+constexpr int kStepSpl = 4;  // states per lane (NS / 4 lanes per channel)
 
-template <typename T>
+template <typename T, int NS>
 __global__ void __launch_bounds__(256) ssm_step_kernel(const T* __restrict__ u, const T* __restrict__ delta,
                                                        const T* __restrict__ A, const T* __restrict__ Bm,
                                                        const T* __restrict__ Cm, const T* __restrict__ Dv,
                                                        const T* h_in, ScanXf xf, T* __restrict__ y,
                                                        T* __restrict__ y_z, T* h_out, int64_t channels, int D) {
+    constexpr int kStepLpc = NS / kStepSpl;
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // over batch * dim * kStepLpc
     const int n0 = (int)(i % kStepLpc) * kStepSpl;
     const int64_t bd = i / kStepLpc;  // b * D + d
@@ -38,10 +38,10 @@ __global__ void __launch_bounds__(256) ssm_step_kernel(const T* __restrict__ u, 
     const float dtu = dt * uu;
     // 4 consecutive states per lane: one 8-byte (fp16) or 16-byte (fp32) access per tensor
     typedef T vec4 __attribute__((ext_vector_type(4)));
-    const vec4 a4 = *reinterpret_cast<const vec4*>(A + (int64_t)d * kNState + n0);
-    const vec4 h4 = *reinterpret_cast<const vec4*>(h_in + bdc * kNState + n0);
-    const vec4 b4 = *reinterpret_cast<const vec4*>(Bm + b * kNState + n0);
-    const vec4 c4 = *reinterpret_cast<const vec4*>(Cm + b * kNState + n0);
+    const vec4 a4 = *reinterpret_cast<const vec4*>(A + (int64_t)d * NS + n0);
+    const vec4 h4 = *reinterpret_cast<const vec4*>(h_in + bdc * NS + n0);
+    const vec4 b4 = *reinterpret_cast<const vec4*>(Bm + b * NS + n0);
+    const vec4 c4 = *reinterpret_cast<const vec4*>(Cm + b * NS + n0);
     vec4 o4;
     float yp = 0.f;
 #pragma unroll
@@ -53,7 +53,7 @@ __global__ void __launch_bounds__(256) ssm_step_kernel(const T* __restrict__ u, 
     }
     const float yv = __builtin_fmaf(ld(Dv + d), uu, group_sum<kStepLpc>(yp));
     if (valid) {
-        *reinterpret_cast<vec4*>(h_out + bdc * kNState + n0) = o4;  // each lane rewrites only what it read
+        *reinterpret_cast<vec4*>(h_out + bdc * NS + n0) = o4;  // each lane rewrites only what it read
         if (n0 == 0) {
             if (y != nullptr) st(y + bdc, yv);
             if (xf.z != nullptr) {
@@ -64,17 +64,27 @@ __global__ void __launch_bounds__(256) ssm_step_kernel(const T* __restrict__ u, 
     }
 }
 
-hipError_t launch_ssm_step(int dt, const void* u, const void* delta, const void* A, const void* B, const void* C,
-                           const void* Dv, const void* h_in, const ScanXf& xf, void* y, void* y_z, void* h_out,
-                           int64_t batch, int64_t dim, hipStream_t st) {
+hipError_t launch_ssm_step(int dt, int ns, const void* u, const void* delta, const void* A, const void* B,
+                           const void* C, const void* Dv, const void* h_in, const ScanXf& xf, void* y, void* y_z,
+                           void* h_out, int64_t batch, int64_t dim, hipStream_t st) {
     const int64_t channels = batch * dim;
-    const int64_t lanes = channels * kStepLpc;
+    const int64_t lanes = channels * (ns / kStepSpl);
     const int grid = (int)((lanes + 255) / 256);
-    MWC_DISPATCH_DTYPE(dt, TT,
-                       hipLaunchKernelGGL(ssm_step_kernel<TT>, dim3(grid), dim3(256), 0, st, (const TT*)u,
-                                          (const TT*)delta, (const TT*)A, (const TT*)B, (const TT*)C, (const TT*)Dv,
-                                          (const TT*)h_in, xf, (TT*)y, (TT*)y_z, (TT*)h_out, channels, (int)dim));
-    return hipGetLastError();
+#define MWC_STEP(N)                                                                                            \
+    if (ns == N) {                                                                                             \
+        MWC_DISPATCH_DTYPE(dt, TT,                                                                             \
+                           hipLaunchKernelGGL((ssm_step_kernel<TT, N>), dim3(grid), dim3(256), 0, st,          \
+                                              (const TT*)u, (const TT*)delta, (const TT*)A, (const TT*)B,      \
+                                              (const TT*)C, (const TT*)Dv, (const TT*)h_in, xf, (TT*)y,        \
+                                              (TT*)y_z, (TT*)h_out, channels, (int)dim));                      \
+        return hipGetLastError();                                                                              \
+    }
+    MWC_STEP(8)
+    MWC_STEP(16)
+    MWC_STEP(32)
+    MWC_STEP(64)
+#undef MWC_STEP
+    return hipErrorInvalidValue;
 }
 
 }  // namespace mwc

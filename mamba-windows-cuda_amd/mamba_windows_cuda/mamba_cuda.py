@@ -1,4 +1,4 @@
-"""Selective scan (Mamba-1, N=16) on MI355X -- the drop-in for
+"""Selective scan (Mamba-1, N=16; also N=8, 32, 64) on MI355X -- the drop-in for
 ``mamba_windows_cuda.mamba_cuda`` of zouyuanqing/mamba-windows-cuda.
 
 Same public names, signatures, shapes and dtype rules as the reference
@@ -16,7 +16,7 @@ reference, all in the direction of correctness:
 
 Checkpoint levels (the memory/speed knob of FusedSelectiveScan,
 selective_scan_cuda_ext.py:573-621, also accepted by SelectiveScanCuda):
-0 = the forward stores the fp32 state every 16 steps (B*ceil(L/16)*D*16*4
+0 = the forward stores the fp32 state every 16 steps (B*ceil(L/16)*D*N*4
 bytes) and the backward restarts from it; 1 = only the inputs are kept and
 the backward first re-runs a state-only forward pass to rebuild them.
 """
@@ -110,8 +110,9 @@ class SelectiveScanCuda(torch.nn.Module):
 
     ``forward(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None) -> out`` and
     ``forward_with_state(...) -> (out, h_last)``. Shapes: u, delta (B, L, D);
-    A (D, 16); B_ssm, C_ssm (B, L, 16); D_ssm (D,); h_prev, h_last (B, D, 16).
-    All tensors fp32 or all fp16, on the GPU; outputs and gradients take the
+    A (D, N); B_ssm, C_ssm (B, L, N); D_ssm (D,); h_prev, h_last (B, D, N), with
+    N = 16 as in the reference, or 8, 32, 64. All tensors fp32 or all fp16 (or
+    all bf16), on the GPU; outputs and gradients take the
     input dtype. ``checkpoint_lvl`` (keyword, default 0) picks the memory/speed
     trade-off described in the module docstring.
 

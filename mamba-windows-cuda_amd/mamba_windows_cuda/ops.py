@@ -4,8 +4,8 @@ torch caching allocator.
 
 The validation restates the reference host wrapper's contract and messages
 (``selective_scan_cuda_forward_with_state``, mamba_windows_cuda/mamba_cuda.py:
-281-326): device, dtype (fp32/fp16, all equal), last-dim contiguity, N == 16,
-ranks and shapes, then the optional h_prev. Violations raise RuntimeError
+281-326): device, dtype (fp32/fp16, all equal), last-dim contiguity, N == 16
+(widened here to N in {8, 16, 32, 64}), ranks and shapes, then the optional h_prev. Violations raise RuntimeError
 before any device work is queued.
 """
 from __future__ import annotations
@@ -15,6 +15,8 @@ import torch
 from . import _lib
 
 NSTATE = 16
+# state counts the kernels are built for (the reference builds N=16 only)
+NSTATES = (8, 16, 32, 64)
 
 
 STORAGE_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
@@ -51,7 +53,8 @@ def check_ssm_inputs(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, *, require_d
         _require(t.dim() == 0 or t.stride(-1) == 1 or t.size(-1) == 1,
                  f"{name} must be contiguous in the last dimension")
     _require(A.dim() == 2, "A must be 2D (dim, state)")
-    _require(A.size(1) == NSTATE, "Only N=16 is supported")
+    _require(A.size(1) in NSTATES, "Only N=16 (or 8, 32, 64) is supported")
+    n = A.size(1)
     _require(u.dim() == 3, "u must be 3D (batch, seqlen, dim)")
     _require(delta.dim() == 3, "delta must be 3D (batch, seqlen, dim)")
     _require(B_ssm.dim() == 3, "B_ssm must be 3D (batch, seqlen, state)")
@@ -59,9 +62,9 @@ def check_ssm_inputs(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, *, require_d
     _require(D_ssm.dim() == 1, "D_ssm must be 1D (dim)")
     bsz, L, dm = u.shape
     _require(tuple(delta.shape) == (bsz, L, dm), "delta shape mismatch")
-    _require(tuple(A.shape) == (dm, NSTATE), "A shape mismatch")
-    _require(tuple(B_ssm.shape) == (bsz, L, NSTATE), "B_ssm shape mismatch")
-    _require(tuple(C_ssm.shape) == (bsz, L, NSTATE), "C_ssm shape mismatch")
+    _require(tuple(A.shape) == (dm, n), "A shape mismatch")
+    _require(tuple(B_ssm.shape) == (bsz, L, n), "B_ssm shape mismatch")
+    _require(tuple(C_ssm.shape) == (bsz, L, n), "C_ssm shape mismatch")
     _require(tuple(D_ssm.shape) == (dm,), "D_ssm shape mismatch")
     devs = {t.device for _, t in named}
     _require(len(devs) == 1, "all inputs must be on the same device")
@@ -72,7 +75,7 @@ def check_ssm_inputs(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, *, require_d
         _require(h_prev.dim() == 0 or h_prev.stride(-1) == 1 or h_prev.size(-1) == 1,
                  "h_prev must be contiguous in the last dimension")
         _require(h_prev.dim() == 3, "h_prev must be 3D (batch, dim, state)")
-        _require(tuple(h_prev.shape) == (bsz, dm, NSTATE), "h_prev shape must be (B, D, N)")
+        _require(tuple(h_prev.shape) == (bsz, dm, n), "h_prev shape must be (B, D, N)")
         _require(h_prev.device == u.device, "h_prev must be on the same device as u")
 
 
@@ -96,7 +99,7 @@ def ssm_forward_xf(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, *, delta_bias=
     """Fused forward with the optional transforms (delta' = softplus(delta + delta_bias),
     out_z = out * silu(z)). Returns (out_z or out, ungated out or None, h_last or None, ckpt or None).
 
-    ckpt is fp32 (B, ceil(L/16), D, 16): the state before every 16th step,
+    ckpt is fp32 (B, ceil(L/16), D, N): the state before every 16th step,
     which the backward restarts from."""
     check_ssm_inputs(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev)
     check_transforms(u, delta_bias, z)
@@ -106,19 +109,20 @@ def ssm_forward_xf(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, *, delta_bias=
     z = None if z is None else z.contiguous()
     L_ = _lib.lib()
     bsz, L, dm = u.shape
+    n = A.size(1)
     dev = u.device
     gated = z is not None
     out = torch.empty_like(u) if (want_out and not gated) or (gated and want_ungated) else None
     out_z = torch.empty_like(u) if gated and want_out else None
-    h_last = torch.empty(bsz, dm, NSTATE, dtype=u.dtype, device=dev) if want_h_last else None
-    ckpt = (torch.empty(bsz, ckpt_count(L), dm, NSTATE, dtype=torch.float32, device=dev)
+    h_last = torch.empty(bsz, dm, n, dtype=u.dtype, device=dev) if want_h_last else None
+    ckpt = (torch.empty(bsz, ckpt_count(L), dm, n, dtype=torch.float32, device=dev)
             if want_ckpt else None)
-    nbytes = L_.mwc_ssm_fwd_workspace_size(bsz, L, dm, NSTATE)
+    nbytes = L_.mwc_ssm_fwd_workspace_size(bsz, L, dm, n)
     ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
         st = L_.mwc_ssm_fwd_ex(_dtype_code(u), _ptr(u), _ptr(delta), _ptr(A), _ptr(B_ssm), _ptr(C_ssm),
                                _ptr(D_ssm), _ptr(h_prev), _ptr(delta_bias), int(bool(delta_softplus)), _ptr(z),
-                               _ptr(out), _ptr(out_z), _ptr(h_last), _ptr(ckpt), bsz, L, dm, NSTATE,
+                               _ptr(out), _ptr(out_z), _ptr(h_last), _ptr(ckpt), bsz, L, dm, n,
                                ws.data_ptr(), nbytes, _stream(dev))
     _lib.check(st, "mwc_ssm_fwd_ex")
     return (out_z if gated else out), (out if gated else None), h_last, ckpt
@@ -139,13 +143,15 @@ def ssm_backward_xf(u, delta, A, B_ssm, C_ssm, D_ssm, dout, ckpt, dh_last=None, 
     (du, ddelta, dA, dB, dC, dD, dh_prev or None, ddelta_bias or None, dz or None), in u's dtype."""
     u, delta, A, B_ssm, C_ssm, D_ssm = (t.contiguous() for t in (u, delta, A, B_ssm, C_ssm, D_ssm))
     bsz, L, dm = u.shape
+    n = A.size(1)
+    _require(n in NSTATES, "Only N=16 (or 8, 32, 64) is supported")
     dout = dout.to(u.dtype).contiguous()
     _require(tuple(dout.shape) == (bsz, L, dm), "dout shape mismatch")
     if dh_last is not None:
         dh_last = dh_last.to(u.dtype).contiguous()
-        _require(tuple(dh_last.shape) == (bsz, dm, NSTATE), "dh_last shape must be (B, D, N)")
+        _require(tuple(dh_last.shape) == (bsz, dm, n), "dh_last shape must be (B, D, N)")
     _require(ckpt is not None and ckpt.dtype == torch.float32 and ckpt.is_contiguous()
-             and tuple(ckpt.shape) == (bsz, ckpt_count(L), dm, NSTATE), "ckpt does not match the inputs")
+             and tuple(ckpt.shape) == (bsz, ckpt_count(L), dm, n), "ckpt does not match the inputs")
     check_transforms(u, delta_bias, z)
     delta_bias = None if delta_bias is None else delta_bias.contiguous()
     if z is not None:
@@ -161,17 +167,17 @@ def ssm_backward_xf(u, delta, A, B_ssm, C_ssm, D_ssm, dout, ckpt, dh_last=None, 
     dB = torch.empty_like(B_ssm)
     dC = torch.empty_like(C_ssm)
     dD = torch.empty_like(D_ssm)
-    dh_prev = torch.empty(bsz, dm, NSTATE, dtype=u.dtype, device=dev) if want_dh_prev else None
+    dh_prev = torch.empty(bsz, dm, n, dtype=u.dtype, device=dev) if want_dh_prev else None
     dbias = torch.empty_like(delta_bias) if delta_bias is not None else None
     dz = torch.empty_like(z) if z is not None else None
-    nbytes = L_.mwc_ssm_bwd_workspace_size(bsz, L, dm, NSTATE)
+    nbytes = L_.mwc_ssm_bwd_workspace_size(bsz, L, dm, n)
     ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
         st = L_.mwc_ssm_bwd_ex(_dtype_code(u), _ptr(u), _ptr(delta), _ptr(A), _ptr(B_ssm), _ptr(C_ssm),
                                _ptr(D_ssm), None, _ptr(delta_bias), int(bool(delta_softplus)), _ptr(z),
                                _ptr(out_ungated if z is not None else None), _ptr(dout), _ptr(dh_last), _ptr(ckpt),
                                _ptr(du), _ptr(ddelta), _ptr(dA), _ptr(dB), _ptr(dC), _ptr(dD), _ptr(dbias),
-                               _ptr(dz), _ptr(dh_prev), bsz, L, dm, NSTATE, ws.data_ptr(), nbytes, _stream(dev))
+                               _ptr(dz), _ptr(dh_prev), bsz, L, dm, n, ws.data_ptr(), nbytes, _stream(dev))
     _lib.check(st, "mwc_ssm_bwd_ex")
     return du, ddelta, dA, dB, dC, dD, dh_prev, dbias, dz
 
@@ -183,8 +189,8 @@ def ssm_backward(u, delta, A, B_ssm, C_ssm, D_ssm, dout, ckpt, dh_last=None, wan
 
 def ssm_step(u, delta, A, B_ssm, C_ssm, D_ssm, h, *, delta_bias=None, delta_softplus=False, z=None,
              out_state=None):
-    """One decode step: u, delta, z (B, D); A (D, 16); B_ssm, C_ssm (B, 16); D_ssm (D,); h (B, D, 16).
-    Returns (out (B, D) -- gated by silu(z) when z is given --, h_new (B, D, 16)). out_state, when
+    """One decode step: u, delta, z (B, D); A (D, N); B_ssm, C_ssm (B, N); D_ssm (D,); h (B, D, N).
+    Returns (out (B, D) -- gated by silu(z) when z is given --, h_new (B, D, N)). out_state, when
     given, receives h_new and may be h itself (in-place update)."""
     named = (("u", u), ("delta", delta), ("A", A), ("B_ssm", B_ssm), ("C_ssm", C_ssm), ("D_ssm", D_ssm), ("h", h))
     for name, t in named:
@@ -193,9 +199,10 @@ def ssm_step(u, delta, A, B_ssm, C_ssm, D_ssm, h, *, delta_bias=None, delta_soft
     _require(u.dtype in STORAGE_DTYPES, "u must be float32/float16 (or bfloat16)")
     _require(u.dim() == 2, "u must be 2D (batch, dim) for a step")
     bsz, dm = u.shape
-    _require(A.dim() == 2 and A.size(1) == NSTATE, "Only N=16 is supported")
-    for name, t, shape in (("delta", delta, (bsz, dm)), ("A", A, (dm, NSTATE)), ("B_ssm", B_ssm, (bsz, NSTATE)),
-                           ("C_ssm", C_ssm, (bsz, NSTATE)), ("D_ssm", D_ssm, (dm,)), ("h", h, (bsz, dm, NSTATE)),
+    _require(A.dim() == 2 and A.size(1) in NSTATES, "Only N=16 (or 8, 32, 64) is supported")
+    n = A.size(1)
+    for name, t, shape in (("delta", delta, (bsz, dm)), ("A", A, (dm, n)), ("B_ssm", B_ssm, (bsz, n)),
+                           ("C_ssm", C_ssm, (bsz, n)), ("D_ssm", D_ssm, (dm,)), ("h", h, (bsz, dm, n)),
                            ("delta_bias", delta_bias, (dm,)), ("z", z, (bsz, dm))):
         if t is not None:
             _require(tuple(t.shape) == shape, f"{name} shape must be {shape}")
@@ -212,16 +219,16 @@ def ssm_step(u, delta, A, B_ssm, C_ssm, D_ssm, h, *, delta_bias=None, delta_soft
     z = None if z is None else z.contiguous()
     if out_state is None:
         out_state = torch.empty_like(h)
-    _require(out_state.is_contiguous() and tuple(out_state.shape) == (bsz, dm, NSTATE) and out_state.dtype == u.dtype
+    _require(out_state.is_contiguous() and tuple(out_state.shape) == (bsz, dm, n) and out_state.dtype == u.dtype
              and out_state.data_ptr() % align == 0,
-             "out_state must be a contiguous, 4-element-aligned (B, D, 16) tensor of u's dtype")
+             "out_state must be a contiguous, 4-element-aligned (B, D, N) tensor of u's dtype")
     out = torch.empty_like(u)
     L_ = _lib.lib()
     with torch.cuda.device(u.device):
         st = L_.mwc_ssm_step(_dtype_code(u), _ptr(u), _ptr(delta), _ptr(A), _ptr(B_ssm), _ptr(C_ssm), _ptr(D_ssm),
                              _ptr(h), _ptr(delta_bias), int(bool(delta_softplus)), _ptr(z),
                              None if z is not None else _ptr(out), _ptr(out) if z is not None else None,
-                             _ptr(out_state), bsz, dm, NSTATE, _stream(u.device))
+                             _ptr(out_state), bsz, dm, n, _stream(u.device))
     _lib.check(st, "mwc_ssm_step")
     return out, out_state
 

@@ -28,19 +28,19 @@ CONFIGS = {
 
 
 def ssm_inputs(B, L, D, *, dtype=torch.float32, a_lo=0.01, a_hi=1.0, d_mode="normal", h_prev=False,
-               dout=True, seed=0, device="cpu", gen_device="cpu"):
-    """Seeded selective-scan inputs. Returns a dict of tensors on `device`."""
+               dout=True, seed=0, device="cpu", gen_device="cpu", nstate=NSTATE):
+    """Seeded selective-scan inputs (state count `nstate`). Returns a dict of tensors on `device`."""
     g = torch.Generator(device=gen_device).manual_seed(seed)
     kw = dict(generator=g, device=gen_device, dtype=torch.float32)
     r = {}
     r["u"] = torch.randn(B, L, D, **kw)
     r["delta"] = 1e-3 + (1e-1 - 1e-3) * torch.rand(B, L, D, **kw)
-    r["A"] = -(a_lo + (a_hi - a_lo) * torch.rand(D, NSTATE, **kw))
-    r["B"] = torch.randn(B, L, NSTATE, **kw)
-    r["C"] = torch.randn(B, L, NSTATE, **kw)
+    r["A"] = -(a_lo + (a_hi - a_lo) * torch.rand(D, nstate, **kw))
+    r["B"] = torch.randn(B, L, nstate, **kw)
+    r["C"] = torch.randn(B, L, nstate, **kw)
     r["D"] = torch.ones(D, device=gen_device) if d_mode == "ones" else 1.0 + 0.1 * torch.randn(D, **kw)
     if h_prev:
-        r["h_prev"] = 0.1 * torch.randn(B, D, NSTATE, **kw)
+        r["h_prev"] = 0.1 * torch.randn(B, D, nstate, **kw)
     if dout:
         r["dout"] = torch.randn(B, L, D, **kw)
     return {k: v.to(device=device, dtype=dtype) for k, v in r.items()}
@@ -60,13 +60,13 @@ def pscan_inputs(shape=(4, 65536, 1024), *, dtype=torch.float32, seed=0, device=
     return a.to(device=device, dtype=dtype), b.to(device=device, dtype=dtype)
 
 
-def algorithmic_bytes(B, L, D, elem_bytes, *, fwd=True, bwd=True, state_io=False):
+def algorithmic_bytes(B, L, D, elem_bytes, *, fwd=True, bwd=True, state_io=False, nstate=NSTATE):
     """Compulsory HBM bytes of the fused path (inputs read once, outputs written once).
 
     fwd = s*(3BLD + 2BLN + DN + D)       (u, delta in; out; B, C; A; D)
     bwd = s*(5BLD + 4BLN + 2DN + 2D)     (u, delta, dout in; du, ddelta out; B, C in; dB, dC out; A, dA; D, dD)
     state_io adds s*2BDN per direction (h_prev in / h_last out, dh_last in / dh_prev out)."""
-    N = NSTATE
+    N = nstate
     s = elem_bytes
     n = 0
     if fwd:

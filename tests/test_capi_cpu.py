@@ -46,9 +46,11 @@ def test_argument_errors_before_any_launch():
 
     L = _lib.lib()
     fake = ctypes.c_void_p(16)
-    # N != 16 (mamba_cuda.py:215)
-    st = L.mwc_ssm_fwd(1, fake, fake, fake, fake, fake, fake, None, fake, None, None, 1, 8, 8, 15, fake, 1 << 20, None)
-    assert st == 1 and b"N=16" in L.mwc_last_error()
+    # N outside {8, 16, 32, 64} (the reference accepts N=16 only, mamba_cuda.py:215)
+    for bad_n in (15, 4, 128):
+        st = L.mwc_ssm_fwd(1, fake, fake, fake, fake, fake, fake, None, fake, None, None, 1, 8, 8, bad_n, fake,
+                           1 << 20, None)
+        assert st == 1 and b"N=16" in L.mwc_last_error()
     # bad dtype
     st = L.mwc_ssm_fwd(7, fake, fake, fake, fake, fake, fake, None, fake, None, None, 1, 8, 8, 16, fake, 1 << 20, None)
     assert st == 1
@@ -106,11 +108,12 @@ def test_step_argument_errors():
     # missing state
     st = L.mwc_ssm_step(0, fake, fake, fake, fake, fake, fake, None, None, 0, None, fake, None, fake, 2, 8, 16, None)
     assert st == 1 and b"h_new" in L.mwc_last_error()
-    # z without out_z, N != 16
+    # z without out_z; an unsupported N
     assert L.mwc_ssm_step(0, fake, fake, fake, fake, fake, fake, fake, None, 0, fake, fake, None, fake, 2, 8, 16,
                           None) == 1
-    assert L.mwc_ssm_step(0, fake, fake, fake, fake, fake, fake, fake, None, 0, None, fake, None, fake, 2, 8, 8,
+    assert L.mwc_ssm_step(0, fake, fake, fake, fake, fake, fake, fake, None, 0, None, fake, None, fake, 2, 8, 12,
                           None) == 1
+    assert b"N=16" in L.mwc_last_error()
 
 
 def test_workspace_sizes_monotone():
@@ -125,6 +128,8 @@ def test_workspace_sizes_monotone():
     assert L.mwc_ssm_fwd_workspace_size(8, 2048, 1536, 16) % 256 == 0
     assert L.mwc_ssm_fwd_workspace_size(1, 131072, 2048, 16) > 0
     assert L.mwc_pscan_workspace_size(4, 65536, 1024) > 0
+    # the carries and the dB/dC/dA partials scale with N
+    assert L.mwc_ssm_bwd_workspace_size(8, 2048, 1536, 8) < a < L.mwc_ssm_bwd_workspace_size(8, 2048, 1536, 64)
 
 
 def _valid(dtype=torch.float32, B=2, L=5, D=3):
@@ -135,6 +140,7 @@ def _valid(dtype=torch.float32, B=2, L=5, D=3):
 
 @pytest.mark.parametrize("mutate,msg", [
     (lambda x: x.update(A=torch.randn(3, 15)), "Only N=16"),
+    (lambda x: x.update(A=torch.randn(3, 32)), "B_ssm shape mismatch"),
     (lambda x: x.update(u=x["u"].double()), "float32/float16"),
     (lambda x: x.update(delta=x["delta"].half()), "delta dtype must match"),
     (lambda x: x.update(u=x["u"][0]), "u must be 3D"),
