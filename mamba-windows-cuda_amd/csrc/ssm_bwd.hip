@@ -110,8 +110,8 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
     constexpr int BCPT = BCN >= 256 ? BCN / 256 : 1;   // of them per loader thread
     static_assert(NSG * SPG == TC && (BCN < 256 || BCN % 256 == 0), "tiling");
 
-    __shared__ float s_in[2][2][CPB][RS];  // [buf][delta, dout][channel][step]
-    __shared__ float s_c[2][TC][NS];
+    __shared__ __align__(16) float s_in[2][2][CPB][RS];  // [buf][delta, dout][channel][step]
+    __shared__ __align__(16) float s_c[2][TC][NS];
 
     const int tid = threadIdx.x;
     const int lid = xcd_remap(blockIdx.x, gridDim.x);
@@ -281,15 +281,16 @@ ssm_bwd_kernel(
     // [delta, delta*u, u, dout] planes of [channel][step]; planes are AS floats apart
     // (AS = 16 mod 64 banks) so the delta*u and dout weights of one channel sit in different banks
     constexpr int AS = CPB * RS + 16;
-    __shared__ float s_in_raw[4 * AS];
-    __shared__ float s_bc[TC][2 * NS];
+    __shared__ __align__(16) float s_in_raw[4 * AS];
+    // B/C rows of the chunk, [step][n / SPL][B x SPL, C x SPL]: a lane reads its B and C with one access
+    __shared__ __align__(16) float s_bc[TC][2 * NS];
     // wave-private slabs of g_t (plane 0) and h_t (plane 1): [wave][plane][slot][channel][16];
     // a 16-lane group deposits 64 consecutive floats, plane 1 is offset by 32 banks
     constexpr int PL = kRedSlots * CPW * NS + 32;
-    __shared__ float s_red[4][2 * PL];
+    __shared__ __align__(16) float s_red[4][2 * PL];
     auto s_in = [&](int plane, int ch) -> float* { return &s_in_raw[plane * AS + ch * RS]; };
-    __shared__ float s_part[4][TC][2 * NS];
-    __shared__ float s_out[2][TC][OS];  // [du, ddelta][step][channel]
+    __shared__ __align__(16) float s_part[4][TC][2 * NS];
+    __shared__ __align__(16) float s_out[2][TC][OS];  // [du, ddelta][step][channel]
     __shared__ int s_flag;              // index of the last staged chunk that needs the exponent clamp
 
     const int tid = threadIdx.x;
@@ -433,8 +434,10 @@ ssm_bwd_kernel(
         for (int q = 0; q < BCPT; ++q) {
             const int e = tid * BCPT + q;
             if (BCN >= 256 || e < BCN) {
-                s_bc[e / NS][e % NS] = static_cast<float>(pb[q]);
-                s_bc[e / NS][NS + e % NS] = static_cast<float>(pc[q]);
+                const int n = e % NS;
+                float* row = &s_bc[e / NS][(n / SPL) * 2 * SPL + n % SPL];
+                row[0] = static_cast<float>(pb[q]);
+                row[SPL] = static_cast<float>(pc[q]);
             }
         }
     };
@@ -482,7 +485,7 @@ ssm_bwd_kernel(
                     for (int q = 0; q < 4; ++q) {
                         const int i = i4 + q;
                         float Bv[SPL];
-                        ldv<SPL>(&s_bc[i][n0], Bv);
+                        ldv<SPL>(&s_bc[i][2 * n0], Bv);
 #pragma unroll
                         for (int j = 0; j < SPL; ++j) {
                             const float x = dt4[q] * A2[j];
@@ -533,8 +536,16 @@ ssm_bwd_kernel(
             ldv<4>(s_in(2, c) + TC - 4, uqn);
             ldv<4>(s_in(3, c) + TC - 4, yqn);
             ldv<4>(s_in(0, c) + TC - 4, dqn);
-            ldv<SPL>(&s_bc[TC - 1][n0], Bn);
-            ldv<SPL>(&s_bc[TC - 1][NS + n0], Cn);
+            auto ld_bc = [&](int i, float (&Bo)[SPL], float (&Co)[SPL]) {
+                float bc[2 * SPL];
+                ldv<2 * SPL>(&s_bc[i][2 * n0], bc);
+#pragma unroll
+                for (int j = 0; j < SPL; ++j) {
+                    Bo[j] = bc[j];
+                    Co[j] = bc[SPL + j];
+                }
+            };
+            ld_bc(TC - 1, Bn, Cn);
 #pragma unroll
             for (int i = TC - 1; i >= 0; --i) {
                 const int slot = i % kRedSlots, phase = i / kRedSlots;
@@ -558,8 +569,7 @@ ssm_bwd_kernel(
                     Cv[j] = Cn[j];
                 }
                 if (i > 0) {
-                    ldv<SPL>(&s_bc[i > 0 ? i - 1 : 0][n0], Bn);
-                    ldv<SPL>(&s_bc[i > 0 ? i - 1 : 0][NS + n0], Cn);
+                    ld_bc(i > 0 ? i - 1 : 0, Bn, Cn);
                 }
                 // keep the next step's operand reads here, a full step ahead of their use (the
                 // scheduler would otherwise sink them next to the use and expose the LDS latency)

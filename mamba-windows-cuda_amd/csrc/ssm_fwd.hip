@@ -95,9 +95,11 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
     constexpr int BCPT = BCN >= 256 ? BCN / 256 : 1;   // of them per loader thread
     static_assert(NSG * SPG == TC && (BCN < 256 || BCN % 256 == 0), "loader tiling");
 
-    __shared__ float s_in[2][2][CPB][RS];  // [buf][delta, delta*u][channel][step]
-    __shared__ float s_bc[2][TC][HAS_OUT ? 2 * NS : NS];
-    __shared__ float s_y[HAS_OUT ? 2 : 1][HAS_OUT ? TC : 1][HAS_OUT ? YS : 1];
+    __shared__ __align__(16) float s_in[2][2][CPB][RS];  // [buf][delta, delta*u][channel][step]
+    // B/C rows of the chunk: with C, each lane's SPL states of B then of C sit together
+    // ([step][n / SPL][B x SPL, C x SPL]) so a lane reads both with one 2*SPL-float access
+    __shared__ __align__(16) float s_bc[2][TC][HAS_OUT ? 2 * NS : NS];
+    __shared__ __align__(16) float s_y[HAS_OUT ? 2 : 1][HAS_OUT ? TC : 1][HAS_OUT ? YS : 1];
 
     const int tid = threadIdx.x;
     const int lid = xcd_remap(blockIdx.x, gridDim.x);
@@ -209,8 +211,14 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
         for (int q = 0; q < BCPT; ++q) {
             const int e = tid * BCPT + q;
             if (BCN >= 256 || e < BCN) {
-                s_bc[buf][e / NS][e % NS] = static_cast<float>(pb[q]);
-                if constexpr (HAS_OUT) s_bc[buf][e / NS][NS + e % NS] = static_cast<float>(pc[q]);
+                const int n = e % NS;
+                if constexpr (HAS_OUT) {
+                    float* row = &s_bc[buf][e / NS][(n / SPL) * 2 * SPL + n % SPL];
+                    row[0] = static_cast<float>(pb[q]);
+                    row[SPL] = static_cast<float>(pc[q]);
+                } else {
+                    s_bc[buf][e / NS][n] = static_cast<float>(pb[q]);
+                }
             }
         }
     };
@@ -240,8 +248,17 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
         lds_ld<TC>(&s_in[buf][1][c][0], dtu);
 #pragma unroll
         for (int i = 0; i < TC; ++i) {
-            lds_ld<SPL>(&s_bc[buf][i][n0], Bv[i]);
-            if constexpr (HAS_OUT) lds_ld<SPL>(&s_bc[buf][i][NS + n0], Cv[i]);
+            if constexpr (HAS_OUT) {
+                float bc[2 * SPL];
+                lds_ld<2 * SPL>(&s_bc[buf][i][2 * n0], bc);
+#pragma unroll
+                for (int j = 0; j < SPL; ++j) {
+                    Bv[i][j] = bc[j];
+                    Cv[i][j] = bc[SPL + j];
+                }
+            } else {
+                lds_ld<SPL>(&s_bc[buf][i][n0], Bv[i]);
+            }
         }
         // |delta*A| <= 88 for the whole chunk (the usual case) -> no clamp needed
         float dmax = 0.f;
