@@ -533,6 +533,9 @@ ssm_bwd_kernel(
         };
         {
             float uq[4], yq[4], dq[4], uqn[4], yqn[4], dqn[4], Bn[SPL], Cn[SPL];
+            // lane g keeps du/ddelta of the steps i with i % LPC == g and writes them after the sweep
+            constexpr int KPL = TC / LPC;
+            float kdu[KPL] = {}, kdd[KPL] = {};
             ldv<4>(s_in(2, c) + TC - 4, uqn);
             ldv<4>(s_in(3, c) + TC - 4, yqn);
             ldv<4>(s_in(0, c) + TC - 4, dqn);
@@ -589,9 +592,15 @@ ssm_bwd_kernel(
                 }
                 r1 = group_sum<LPC>(r1);
                 r2 = group_sum<LPC>(r2);
-                // every lane of the group holds the sums; duplicate LDS writes are identical
-                s_out[0][i][c] = __builtin_fmaf(Dd, yo, dti * r1);
-                s_out[1][i][c] = __builtin_fmaf(ui, r1, r2);
+                // every lane of the group holds the sums
+                {
+                    const float vdu = __builtin_fmaf(Dd, yo, dti * r1), vdd = __builtin_fmaf(ui, r1, r2);
+                    const bool mine = g == i % LPC;
+                    kdu[i / LPC] = mine ? vdu : kdu[i / LPC];
+                    kdd[i / LPC] = mine ? vdd : kdd[i / LPC];
+                    // select now: the two step values are dead after this step
+                    asm volatile("" : "+v"(kdu[i / LPC]), "+v"(kdd[i / LPC]));
+                }
                 dDacc = __builtin_fmaf(yo, ui, dDacc);
                 const int sl = slot * CPW + cw;
                 stv<SPL>(red_g + sl * NS + n0, gt);
@@ -601,6 +610,11 @@ ssm_bwd_kernel(
                     fold(phase);
                     wave_lds_fence();
                 }
+            }
+#pragma unroll
+            for (int q = 0; q < KPL; ++q) {
+                s_out[0][q * LPC + g][c] = kdu[q];
+                s_out[1][q * LPC + g][c] = kdd[q];
             }
         }
         __syncthreads();  // every wave is done with the staged chunk and has written s_out / s_part
