@@ -599,7 +599,7 @@ ssm_bwd_kernel(
                     kdu[i / LPC] = mine ? vdu : kdu[i / LPC];
                     kdd[i / LPC] = mine ? vdd : kdd[i / LPC];
                     // select now: the two step values are dead after this step
-                    asm volatile("" : "+v"(kdu[i / LPC]), "+v"(kdd[i / LPC]));
+                    asm("" : "+v"(kdu[i / LPC]), "+v"(kdd[i / LPC]));
                 }
                 dDacc = __builtin_fmaf(yo, ui, dDacc);
                 const int sl = slot * CPW + cw;

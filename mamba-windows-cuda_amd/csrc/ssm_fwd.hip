@@ -287,7 +287,7 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
                     // every lane of the group holds the sum
                     const float ys = group_sum<LPC>(y);
                     ky[i / LPC] = g == i % LPC ? ys : ky[i / LPC];
-                    asm volatile("" : "+v"(ky[i / LPC]));  // select now: ys is dead after this step
+                    asm("" : "+v"(ky[i / LPC]));  // select now: ys is dead after this step
                 }
             }
         };
