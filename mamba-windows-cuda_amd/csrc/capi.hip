@@ -160,31 +160,12 @@ SegPlan plan_bwd(const SsmShape& s) {
     return plan(s, true, spl, n16 ? bwd_cap(spl) : 2, n16 ? bwd_carry_cap(spl) : 2, 0.3);
 }
 
-// Kernel family: 2 = lane groups (ssm_fwd.hip / ssm_bwd.hip, the default), 3 = state groups across
-// waves (ssm_v3.hip; selectable with MWC_IMPL=3 while it is slower at the benchmark shapes).
-int impl_choice() {
-    static const int v = [] {
-        const char* e = getenv("MWC_IMPL");
-        return (e && atoi(e) == 3) ? 3 : 2;
-    }();
-    return v;
-}
-
 size_t fwd_workspace_bytes(const SsmShape& s) {
-    // the state-group kernels read a packed fp32 copy of B/C; the lane-group kernels need the
-    // segment carries when L is split
-    if (impl_choice() == 3) return v3_bcp_bytes(s);
+    // the segment carries when L is split
     return 2 * carry_bytes(s, plan_fwd(s));
 }
 
 size_t bwd_workspace_bytes(const SsmShape& s) {
-    if (impl_choice() == 3) {
-        size_t n = v3_bcp_bytes(s);
-        n += align256((size_t)v3_groups(s) * s.batch * s.seqlen * 32 * sizeof(float));
-        n += align256((size_t)s.batch * s.dim * s.nstate * sizeof(float));
-        n += align256((size_t)s.batch * s.dim * sizeof(float));
-        return n;
-    }
     const SegPlan p = plan_bwd(s);
     size_t n = align256((size_t)bwd_groups(s, s.nstate, p.spl) * s.batch * s.seqlen * 2 * s.nstate *
                         sizeof(float));                                                          // dB/dC
@@ -238,21 +219,11 @@ int mwc_ssm_fwd_ex(int dtype, const void* u, const void* delta, const void* A, c
     if (seqlen > 0 && (!u || !delta || !B_ssm || !C_ssm))
         return fail(MWC_ERR_INVALID_ARGUMENT, "u, delta, B_ssm and C_ssm must not be NULL");
     if (z == nullptr && out_z != nullptr) return fail(MWC_ERR_INVALID_ARGUMENT, "out_z needs z");
-    const bool xf = delta_bias != nullptr || delta_softplus != 0 || z != nullptr;
     const mwc::SsmShape s{batch, seqlen, dim, (int)dstate};
-    const bool half = dtype == MWC_DTYPE_F16;
     hipStream_t st = (hipStream_t)stream;
     const size_t need = mwc::fwd_workspace_bytes(s);
     if (seqlen > 0 && need > 0 && (workspace == nullptr || workspace_bytes < need))
         return fail(MWC_ERR_WORKSPACE, "forward workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
-    if (mwc::impl_choice() == 3) {
-        if (xf || dtype == MWC_DTYPE_BF16 || dstate != 16)
-            return fail(MWC_ERR_UNSUPPORTED, "delta_bias, delta_softplus, z, bf16 and N != 16 need the default kernels");
-        float* bcp = (float*)workspace;
-        if (seqlen > 0) MWC_HIP_TRY(mwc::launch_v3_pack(half, B_ssm, C_ssm, bcp, s, st));
-        MWC_HIP_TRY(mwc::launch_v3_fwd(half, u, delta, A, bcp, D_ssm, h_prev, out, h_last, ckpt, s, st));
-        return MWC_OK;
-    }
     const mwc::SegPlan p = mwc::plan_fwd(s);
     float* car_h = (float*)workspace;
     float* car_x = (float*)((char*)workspace + need / 2);
@@ -288,32 +259,12 @@ int mwc_ssm_bwd_ex(int dtype, const void* u, const void* delta, const void* A, c
         return fail(MWC_ERR_INVALID_ARGUMENT, "out (ungated) and dz must not be NULL when z is given");
     if (ddelta_bias != nullptr && delta_bias == nullptr)
         return fail(MWC_ERR_INVALID_ARGUMENT, "ddelta_bias needs delta_bias");
-    const bool xf = delta_bias != nullptr || delta_softplus != 0 || z != nullptr;
     const mwc::SsmShape s{batch, seqlen, dim, (int)dstate};
     const size_t need = mwc::bwd_workspace_bytes(s);
     if (workspace == nullptr || workspace_bytes < need)
         return fail(MWC_ERR_WORKSPACE, "backward workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
-    const bool half = dtype == MWC_DTYPE_F16;
     hipStream_t st = (hipStream_t)stream;
     char* w = (char*)workspace;
-    if (mwc::impl_choice() == 3) {
-        if (xf || dtype == MWC_DTYPE_BF16 || dstate != 16)
-            return fail(MWC_ERR_UNSUPPORTED, "delta_bias, delta_softplus, z, bf16 and N != 16 need the default kernels");
-        const int ngrp = mwc::v3_groups(s);
-        float* bcp = (float*)w;
-        w += mwc::v3_bcp_bytes(s);
-        float* dbc_part = (float*)w;
-        w += align256((size_t)ngrp * batch * seqlen * 32 * sizeof(float));
-        float* dA_part = (float*)w;
-        w += align256((size_t)batch * dim * mwc::kNState * sizeof(float));
-        float* dD_part = (float*)w;
-        if (seqlen > 0) MWC_HIP_TRY(mwc::launch_v3_pack(half, B_ssm, C_ssm, bcp, s, st));
-        MWC_HIP_TRY(mwc::launch_v3_bwd(half, u, delta, A, bcp, D_ssm, dout, dh_last, ckpt, du, ddelta, dh_prev,
-                                       dA_part, dD_part, dbc_part, s, st));
-        MWC_HIP_TRY(mwc::launch_bwd_finish(dtype, 16, dbc_part, dA_part, dD_part, nullptr, dB, dC, dA, dD, nullptr, ngrp,
-                                           (int)batch, s, st));
-        return MWC_OK;
-    }
     const mwc::SegPlan p = mwc::plan_bwd(s);
     const int ngrp = mwc::bwd_groups(s, s.nstate, p.spl);
     float* dbc_part = (float*)w;

@@ -81,20 +81,6 @@ hipError_t launch_ssm_step(int dt, int ns, const void* u, const void* delta, con
                            const void* C, const void* Dv, const void* h_in, const ScanXf& xf, void* y, void* y_z,
                            void* h_out, int64_t batch, int64_t dim, hipStream_t st);
 
-// "state groups across waves" kernels (ssm_v3.hip)
-int impl_choice();  // 2 = lane groups (default), 3 = state groups across waves
-size_t v3_bcp_bytes(const SsmShape& s);
-int v3_groups(const SsmShape& s);
-hipError_t launch_v3_pack(bool is_half, const void* B, const void* C, float* bcp, const SsmShape& s,
-                          hipStream_t st);
-hipError_t launch_v3_fwd(bool is_half, const void* u, const void* delta, const void* A, const float* bcp,
-                         const void* Dv, const void* h_prev, void* out, void* h_last, float* ckpt,
-                         const SsmShape& s, hipStream_t st);
-hipError_t launch_v3_bwd(bool is_half, const void* u, const void* delta, const void* A, const float* bcp,
-                         const void* Dv, const void* dout, const void* dh_last, const float* ckpt, void* du,
-                         void* ddelta, void* dh_prev, float* dA_part, float* dD_part, float* dbc_part,
-                         const SsmShape& s, hipStream_t st);
-
 hipError_t launch_pscan_fwd(int dt, const void* A, const void* X, void* H, int64_t nseq,
                             int64_t seqlen, int64_t ncols, void* ws, hipStream_t st);
 hipError_t launch_pscan_bwd(int dt, const void* A, const void* H, const void* dH, void* dA,
