@@ -87,20 +87,28 @@ int env_int(const char* name, int lo, int hi) {
     return (v >= lo && v <= hi) ? v : 0;
 }
 
-// Relative throughput of a SIMD running q of these (issue- and latency-bound) waves at once.
+// Relative throughput of a SIMD running q of these (issue- and latency-bound) waves at once
+// (measured on the config-2 / config-3 kernels: a second wave doubles it, a third adds ~8%).
 double simd_throughput(int64_t q) {
-    static const double t[] = {0.0, 1.0, 1.7, 2.2, 2.5};
-    return q < 5 ? t[q] : 2.6;
+    static const double t[] = {0.0, 1.0, 2.0, 2.15, 2.3};
+    return q < 5 ? t[q] : 2.4;
 }
 
 // Duration, in units of one chunk of one lone wave, of a pass of `wgs` equal workgroups of
-// `chunks` chunks each when a CU holds at most `cap` of them at once.
+// `chunks` chunks each when a CU holds at most `cap` of them at once: full rounds of `cap`, then
+// a last round as deep as its busiest CU. Grids of more than one round run a little faster per
+// round than one lock-step round (measured): workgroups that start at different times overlap
+// their LDS-heavy and VALU-heavy phases.
 double pass_time(int64_t wgs, int64_t chunks, int cap) {
     if (wgs <= 0 || chunks <= 0) return 0.0;
-    const int64_t m = (wgs + kCUs - 1) / kCUs;  // workgroups on the busiest CU
-    const int64_t r = (m + cap - 1) / cap;      // rounds
-    const int64_t q = (m + r - 1) / r;          // workgroups per CU in a round
-    return (double)r * ((double)chunks * q / simd_throughput(q) + 1.0);  // +1: prologue, first loads
+    const int64_t full = wgs / (kCUs * cap);
+    const int64_t rem = wgs - full * kCUs * cap;
+    double t = (double)full * ((double)chunks * cap / simd_throughput(cap) + 1.0);  // +1: prologue, first loads
+    if (rem > 0) {
+        const int64_t q = (rem + kCUs - 1) / kCUs;
+        t += (double)chunks * q / simd_throughput(q) + 1.0;
+    }
+    return full + (rem > 0 ? 1 : 0) > 1 ? 0.96 * t : t;
 }
 
 int cpb_of(int ns, int spl) { return 4 * 64 / (ns / spl); }
@@ -118,7 +126,8 @@ SegPlan plan(const SsmShape& s, bool bwd, int spl, int cap_main, int cap_carry, 
     if (force_n == 1 || nck < 2) return best;
     const int n_lo = force_n ? force_n : 2, n_hi = force_n ? force_n : 16;
     for (int n = n_lo; n <= n_hi; ++n) {
-        for (int f = force_f ? force_f : 1; f <= (force_f ? force_f : 8); f *= 2) {
+        // finer carry splits first: they are measured as fast or faster than the model says
+        for (int f = force_f ? force_f : 4; f >= (force_f ? force_f : 1); f /= 2) {
             const int64_t cps = ((nck + n - 1) / n + f - 1) / f * f;  // chunks per segment, a multiple of f
             const int64_t nseg = (nck + cps - 1) / cps;                 // non-empty segments
             if (nseg < 2) continue;
@@ -151,7 +160,7 @@ size_t carry_bytes(const SsmShape& s, const SegPlan& p) {
 SegPlan plan_fwd(const SsmShape& s) {
     const int spl = choose_spl(s.batch * s.dim, s.nstate);
     const bool n16 = s.nstate == 16;
-    return plan(s, false, spl, n16 ? fwd_cap(spl) : 2, n16 ? fwd_carry_cap(spl) : 2, 0.6);
+    return plan(s, false, spl, n16 ? fwd_cap(spl) : 2, n16 ? fwd_carry_cap(spl) : 2, 0.75);
 }
 
 SegPlan plan_bwd(const SsmShape& s) {

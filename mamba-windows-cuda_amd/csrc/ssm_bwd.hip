@@ -328,6 +328,7 @@ ssm_bwd_kernel(
         gc[j] = dh_last != nullptr ? ld(dh_last + ((int64_t)b * D + d) * NS + n0 + j) : 0.f;
         dAacc[j] = 0.f;
     }
+#pragma unroll 4
     for (int j = ncar - 1; j >= seg * cfold; --j) {  // g -> 2^xsum * g + G of each following carry segment
         const int64_t o = (((int64_t)b * ncar + j) * D + d) * NS + n0;
         float cg[SPL], cx[SPL];
@@ -716,20 +717,28 @@ __global__ void __launch_bounds__(256) bwd_finish_kernel(const float* __restrict
     }
     const int64_t i = (int64_t)(blockIdx.x - nblk_bc) * 256 + threadIdx.x;
     const int64_t nA = (int64_t)D * NS;
-    if (i < nA) {
+    // sum of rows 0..nrows-1 in order; eight loads are in flight before their adds
+    auto rows_sum = [nrows](const float* p, int64_t stride) {
         float s = 0.f;
-        for (int r = 0; r < nrows; ++r) s += dA_part[(int64_t)r * nA + i];
-        st(dA + i, s);
+        int r = 0;
+        for (; r + 8 <= nrows; r += 8) {
+            float v[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) v[q] = p[(int64_t)(r + q) * stride];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) s += v[q];
+        }
+        for (; r < nrows; ++r) s += p[(int64_t)r * stride];
+        return s;
+    };
+    if (i < nA) {
+        st(dA + i, rows_sum(dA_part + i, nA));
     } else if (i < nA + D) {
         const int64_t dd = i - nA;
-        float s = 0.f;
-        for (int r = 0; r < nrows; ++r) s += dD_part[(int64_t)r * D + dd];
-        st(dD + dd, s);
+        st(dD + dd, rows_sum(dD_part + dd, D));
     } else if (dbias != nullptr && i < nA + 2 * D) {
         const int64_t dd = i - nA - D;
-        float s = 0.f;
-        for (int r = 0; r < nrows; ++r) s += dbias_part[(int64_t)r * D + dd];
-        st(dbias + dd, s);
+        st(dbias + dd, rows_sum(dbias_part + dd, D));
     }
 }
 

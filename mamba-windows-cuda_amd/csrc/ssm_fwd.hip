@@ -137,6 +137,7 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
         xs[j] = 0.f;
     }
     if constexpr (!CARRY) {
+#pragma unroll 4
         for (int j = 0; j < seg * cfold; ++j) {  // h -> 2^xsum * h + h_end of each preceding carry segment
             float ch[SPL], cx[SPL];
             lds_ld<SPL>(car_h + car0 + j * car_seg, ch);
