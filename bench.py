@@ -7,7 +7,7 @@ storage / fp32 compute, B=8, L=2048, D=1536, N=16; one step = fused forward
 all inputs resident in HBM. Prints ONE JSON line.
 
   python bench.py [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4a|cfg4b]
-                  [--level 0|1] [--skip-cpu] [--transforms] [--decode [BATCH]]
+                  [--level 0|1] [--skip-cpu] [--transforms] [--decode [BATCH]] [--shard K]
 
 `value` = B*L*D / ms_per_step (elements/s). `roofline` covers the dominant
 kernel (the fused backward call), timed live with HIP events on the stream
@@ -31,6 +31,12 @@ for _p in (ROOT, os.path.join(ROOT, "mamba-windows-cuda_amd")):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E peak
+# non-packed fp32 VALU issue: 256 CUs x 64 lanes x 2.4 GHz, in 1e12 lane-operations per second
+VALU_PEAK_TOPS = 256 * 64 * 2.4e9 / 1e12
+# algorithmic VALU issue slots per state and step (v_exp_f32 counted as two): forward = mul
+# (delta*A), exp, mul (delta*u*B), fma (state), fma (C-contraction); backward = the recompute
+# (mul, exp, mul, fma) + the reverse sweep (fma, fma, mul, mul, fma, fma) + the dB/dC fold (2 fma)
+VALU_SLOTS_FWD, VALU_SLOTS_BWD = 6, 13
 METRIC = "fwd+bwd elements/sec (B·L·D) and achieved HBM GB/s vs peak, 1×MI355X"
 
 
@@ -58,15 +64,19 @@ def _events_ms(fn, n):
     return a.elapsed_time(b) / n
 
 
-def bench_ssm(cfg, steps, warmup, level):
+def bench_ssm(cfg, steps, warmup, level, shard=1):
     import torch
 
     from mamba_windows_cuda import SelectiveScanCuda, ops, workloads
 
     c = workloads.CONFIGS[cfg]
-    B, L, D = c["B"], c["L"], c["D"]
+    B, L, D = c["B"], c["L"], c["D"] // shard
     dtype = c["dtype"]
-    x = workloads.config_inputs(cfg, device="cuda", gen_device="cuda")
+    if shard == 1:
+        x = workloads.config_inputs(cfg, device="cuda", gen_device="cuda")
+    else:  # one GPU's channels when D is split over `shard` GPUs
+        kw = {k: v for k, v in c.items() if k not in ("B", "L", "D")}
+        x = workloads.ssm_inputs(B, L, D, device="cuda", gen_device="cuda", **kw)
     leaves = {k: x[k].requires_grad_(True) for k in ("u", "delta", "A", "B", "C", "D")}
     dout = x["dout"]
     m = SelectiveScanCuda(checkpoint_lvl=level)
@@ -121,12 +131,19 @@ def bench_ssm(cfg, steps, warmup, level):
         "dtype": "f32",
         "storage_dtype": "f16" if s == 2 else "f32",
         "config": {"workload": f"{cfg}: selective scan fwd+bwd (fused), B={B} L={L} D={D} N=16, "
-                               f"checkpoint_lvl={level}", "B": B, "L": L, "D": D, "N": 16,
-                   "checkpoint_lvl": level},
+                               f"checkpoint_lvl={level}"
+                               + (f"; one GPU's share of D={c['D']} split over {shard} GPUs" if shard > 1 else ""),
+                   "B": B, "L": L, "D": D, "N": 16, "checkpoint_lvl": level},
         "roofline": {"bound": "hbm", "kernel": "ssm_bwd (fused backward call)",
                      "achieved": gbs_bwd, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": gbs_bwd / HBM_PEAK_GBS, "traffic": _traffic_from_profiles(f"ssm_bwd_{cfg}"),
+                     "frac": gbs_bwd / HBM_PEAK_GBS, "traffic": _traffic_from_profiles(f"ssm_bwd_{cfg}") if shard == 1 else None,
                      "algorithmic_bytes_per_launch": bytes_bwd, "avg_launch_ms": bwd_ms},
+        "valu_roofline": {"bound": "valu", "kernel": "ssm_bwd (fused backward call)",
+                          "achieved": B * L * D * 16 * VALU_SLOTS_BWD / (bwd_ms * 1e-3) / 1e12,
+                          "peak": VALU_PEAK_TOPS, "unit": "T lane-op/s",
+                          "frac": B * L * D * 16 * VALU_SLOTS_BWD / (bwd_ms * 1e-3) / 1e12 / VALU_PEAK_TOPS,
+                          "slots_per_state": VALU_SLOTS_BWD,
+                          "fwd_frac": B * L * D * 16 * VALU_SLOTS_FWD / (fwd_ms * 1e-3) / 1e12 / VALU_PEAK_TOPS},
         "kernels": {"ssm_fwd_ms": fwd_ms, "ssm_bwd_ms": bwd_ms,
                     "fwd_algorithmic_GBps": bytes_fwd / (fwd_ms * 1e-3) / 1e9},
         "step_hbm": {"algorithmic_bytes": bytes_fwd + bytes_bwd, "achieved_GBps": gbs_step,
@@ -134,6 +151,8 @@ def bench_ssm(cfg, steps, warmup, level):
         "wall_ms_per_step": wall_ms,
         "retained_after_forward_GB": kept / 1e9,
     }
+    if shard > 1:  # what the shards would exchange: one all-reduce of the dB/dC partials (fp32)
+        res["shard"] = {"gpus": shard, "split": "D", "allreduce_bytes": 2 * B * L * 16 * 4}
     return res
 
 
@@ -355,6 +374,8 @@ def main():
                     help="time the L=1 decode step at the config's D (batch defaults to the config's)")
     ap.add_argument("--transforms", action="store_true",
                     help="time the scan call with delta_bias/softplus/z gating fused vs. as torch passes")
+    ap.add_argument("--shard", type=int, default=1, choices=[1, 2, 4, 8],
+                    help="time one GPU's share of the config when D is split over this many GPUs")
     ap.add_argument("--kernels-only", action="store_true",
                     help="profiling driver: fused calls, cfg4b scan and a 1 GiB copy; no timing")
     args = ap.parse_args()
@@ -382,8 +403,10 @@ def main():
     elif args.config == "cfg4a":
         res = bench_stream(args.steps, args.warmup)
     else:
-        res = bench_ssm(args.config, args.steps, args.warmup, args.level)
+        res = bench_ssm(args.config, args.steps, args.warmup, args.level, args.shard)
         res["peak_hbm_allocated_GB"] = torch.cuda.max_memory_allocated() / 1e9
+        if args.shard > 1:
+            args.skip_cpu = True
     res.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
                 "scaling": "weak", "vs_baseline": None, "data": "synthetic (seeded; BASELINE.json distributions)",
                 "device": torch.cuda.get_device_name(0)})
