@@ -7,7 +7,6 @@
 
 namespace mwc {
 
-constexpr int kNState = 16;          // the reference's N_STATE (mamba_cuda.py:62)
 constexpr int kCkptSteps = MWC_CKPT_STEPS;
 constexpr float kLog2e = 1.4426950408889634f;
 // safe_exp clamps delta*A to [-88, 88] (mamba_cuda.py:65-70); in base 2 that is +-88*log2(e).

@@ -5,8 +5,9 @@
 //   dA = exp(clamp(delta*A, -88, 88)); h = dA*h + delta*u*B; y = sum_n C*h + D*u.
 //
 // Mapping (not the reference's one-warp-per-channel serial loop): a channel's
-// 16 states are spread over a group of LPC = 16/SPL consecutive lanes, each
-// lane holding SPL states in VGPRs; a 64-lane wave scans 64/LPC channels and a
+// N states (16 in the reference; 8, 32 and 64 are built too) are spread over a
+// group of LPC = N/SPL consecutive lanes, each lane holding SPL states in
+// VGPRs; a 64-lane wave scans 64/LPC channels and a
 // 4-wave workgroup CPB = 4*64/LPC channels of one batch row, walking its part
 // of L in chunks of 16 steps. The C-contraction is an in-register FMA chain
 // plus a DPP all-reduce inside the lane group.
@@ -21,7 +22,7 @@
 // segment.
 //
 // Data movement: the workgroup stages each chunk's inputs through LDS --
-// delta, delta*u and u as fp32 rows per channel (converted once, read back by
+// delta and delta*u as fp32 rows per channel (converted once, read back by
 // the lanes as 128-bit vectors) and the chunk's B/C rows -- double-buffered,
 // with the next chunk's global loads issued before the current chunk is
 // computed, so one barrier per chunk is the only synchronisation. Outputs go

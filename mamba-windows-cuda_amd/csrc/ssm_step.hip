@@ -3,7 +3,7 @@
 // Semantics: the reference's forward_with_state (mamba_cuda.py:271-359) at seqlen 1, i.e.
 //   h' = exp(clamp(delta*A, -88, 88)) * h + delta*u*B;  y = sum_n C*h' + D*u
 // with the optional transforms of the fused scan (delta' = softplus(delta + delta_bias),
-// y_z = y * silu(z)). The state is read and written in the input dtype, (batch, dim, 16), and the
+// y_z = y * silu(z)). The state is read and written in the input dtype, (batch, dim, N), and the
 // output state may alias the input one (in-place update).
 //
 // Mapping: N/4 consecutive lanes hold one channel's N states, 4 per lane, so the state moves as
