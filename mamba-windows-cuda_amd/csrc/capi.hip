@@ -259,7 +259,19 @@ int mwc_ssm_bwd_ex(int dtype, const void* u, const void* delta, const void* A, c
     g_err[0] = 0;
     (void)h_prev;  // the checkpoints already carry h_prev (checkpoint 0)
     if (int st = check_dims(dtype, batch, seqlen, dim, dstate)) return st;
-    if (batch == 0 || dim == 0) return MWC_OK;
+    if (batch == 0 || dim == 0) {
+        // nothing to scan, but sums over an empty batch (dA, dD, d delta_bias) or over no channels
+        // (dB, dC) are zeros: the finishing kernel writes them from zero partials
+        const bool sums_d = dim > 0, sums_bl = batch > 0 && seqlen > 0;
+        if (!sums_d && !sums_bl) return MWC_OK;
+        if (sums_d && (!dA || !dD)) return fail(MWC_ERR_INVALID_ARGUMENT, "dA and dD must not be NULL");
+        if (sums_bl && (!dB || !dC)) return fail(MWC_ERR_INVALID_ARGUMENT, "dB and dC must not be NULL");
+        const mwc::SsmShape s{batch, seqlen, dim, (int)dstate};
+        MWC_HIP_TRY(mwc::launch_bwd_finish(dtype, s.nstate, nullptr, nullptr, nullptr, nullptr, dB, dC, dA, dD,
+                                           delta_bias != nullptr ? ddelta_bias : nullptr, 0, 0, s,
+                                           (hipStream_t)stream));
+        return MWC_OK;
+    }
     if (!A || !D_ssm || !dA || !dD) return fail(MWC_ERR_INVALID_ARGUMENT, "A, D_ssm, dA and dD must not be NULL");
     if (seqlen > 0 && (!u || !delta || !B_ssm || !C_ssm || !dout || !ckpt || !du || !ddelta || !dB || !dC))
         return fail(MWC_ERR_INVALID_ARGUMENT,

@@ -410,3 +410,26 @@ def test_config4a_streaming_long_sequence(dev):
     _close("h_last", h[:, :256], rh, torch.float32)
     _close("out", torch.cat(outs, 1), ro, torch.float32)
     _close("out_full", full_out[:, :, :256], ro, torch.float32)
+
+
+@pytest.mark.parametrize("shape", [(2, 0, 64), (0, 5, 64), (3, 5, 0), (1, 1, 1), (1, 17, 3)])
+def test_empty_and_tiny_shapes(dev, shape):
+    """Empty batch, sequence or channel axes and one-element shapes: outputs of the right shapes,
+    h_last = h_prev and dh_prev = dh_last when L = 0, zero sums over an empty batch (dA, dD) or
+    channel set (dB, dC), and the oracle wherever there is something to compute."""
+    B, L, D = shape
+    print(f"case empty/tiny shape={shape}", flush=True)
+    x = workloads.ssm_inputs(B, L, D, dtype=torch.float32, h_prev=True, seed=B + L + D + 40)
+    dhl = torch.randn(B, D, 16, generator=torch.Generator().manual_seed(41))
+    out, h_last, g = _run(x, dev, with_h=True, dh_last=dhl)
+    assert tuple(out.shape) == (B, L, D) and tuple(h_last.shape) == (B, D, 16)
+    ro, rh = orc.ssm_fwd(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["h_prev"], clamp=True)
+    _close("out", out, ro, torch.float32)
+    _close("h_last", h_last, rh, torch.float32)
+    if L == 0:
+        assert torch.equal(h_last.cpu(), x["h_prev"])
+        assert torch.equal(g["h_prev"].cpu(), dhl)
+    r = orc.ssm_bwd(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["dout"], x["h_prev"], dhl, clamp=True)
+    for k, name in GRADS + (("h_prev", "dh_prev"),):
+        assert tuple(g[k].shape) == tuple(x[k].shape), name
+        _close(name, g[k], r[name], torch.float32)
