@@ -114,6 +114,55 @@ template <int G> __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// Reduce-scatter over aligned groups of G lanes (G in {2,4,8,16}) of V values per lane (V a power of
+// two, 2 <= V <= G): the lane returns the group sum of value rs_index<V>(lane); each index is held by
+// G/V lanes of the group. Level l pairs a lane with its DPP partner of group_sum (xor 1, xor 2, mirror
+// in 8, mirror in 16). At the first log2(V) levels the pair splits its values by a lane bit b_l that
+// differs between the partners and agrees on every lower level's bit -- b0 = i0^i2, b1 = i1^i2,
+// b2 = i2^i3, b3 = i3 for lane i of a 16-lane row -- each keeping one half and adding the partner's
+// copy of it (two selects and one DPP add per pair, against one DPP add per value and level for V
+// separate group sums); the remaining levels add the single value.
+__device__ __forceinline__ int rs_bit(int level, int lane) {
+    const int x = lane & 15;
+    const int i2 = (x >> 2) & 1, i3 = (x >> 3) & 1;
+    return level == 0 ? ((x & 1) ^ i2) : level == 1 ? (((x >> 1) & 1) ^ i2) : level == 2 ? (i2 ^ i3) : i3;
+}
+template <int V> __device__ __forceinline__ int rs_index(int lane) {
+    int idx = 0;
+#pragma unroll
+    for (int l = 0; (1 << l) < V; ++l) idx |= rs_bit(l, lane) << l;
+    return idx;
+}
+template <int L> __device__ __forceinline__ float dpp_level(float v) {
+    if constexpr (L == 0) return dpp<kDppXor1>(v);
+    if constexpr (L == 1) return dpp<kDppXor2>(v);
+    if constexpr (L == 2) return dpp<kDppHalfMirror>(v);
+    if constexpr (L == 3) return dpp<kDppMirror>(v);
+}
+template <int G, int V, int L = 0, int M = V>
+__device__ __forceinline__ float reduce_scatter_lv(float (&x)[V], int lane) {
+    static_assert(V >= 2 && V <= G && (V & (V - 1)) == 0 && (G & (G - 1)) == 0 && G <= 16, "shape");
+    if constexpr ((1 << L) >= G) {
+        return x[0];
+    } else if constexpr (M > 1) {
+        const bool hi = rs_bit(L, lane) != 0;
+#pragma unroll
+        for (int q = 0; q < M / 2; ++q) {
+            const float keep = hi ? x[2 * q + 1] : x[2 * q];
+            const float send = hi ? x[2 * q] : x[2 * q + 1];
+            x[q] = keep + dpp_level<L>(send);
+        }
+        return reduce_scatter_lv<G, V, L + 1, M / 2>(x, lane);
+    } else {
+        x[0] += dpp_level<L>(x[0]);
+        return reduce_scatter_lv<G, V, L + 1, 1>(x, lane);
+    }
+}
+// x is clobbered.
+template <int G, int V> __device__ __forceinline__ float reduce_scatter(float (&x)[V], int lane) {
+    return reduce_scatter_lv<G, V>(x, lane);
+}
+
 }  // namespace mwc
 
 #define MWC_HIP_TRY(expr)                                  \

@@ -337,8 +337,6 @@ ssm_bwd_kernel(
 #pragma unroll
         for (int q = 0; q < SPL; ++q) gc[q] = __builtin_fmaf(__builtin_amdgcn_exp2f(cx[q]), gc[q], cg[q]);
     }
-    float dDacc = 0.f;
-    const float Dd = ld(Dv + d);
     const float* ckb = ckpt + ((int64_t)b * nck * D + d) * NS + n0;
 
     // Chunk k's rows are read through buffer resources spanning exactly its min(16, L - 16k) rows:
@@ -390,6 +388,12 @@ ssm_bwd_kernel(
     // d delta / d delta' (softplus) of the loader's elements, for the chunk being stored and the next
     float dd_cur[XF ? SPG : 1], dd_nxt[XF ? SPG : 1];
     float dbias_acc = 0.f;
+    // the loader's (channel, steps) elements of the chunk being stored and of the next one: delta and
+    // dout (as the scan sees them), for du = D*dout + delta*sum_n g*B; dD accumulates here, once per
+    // element
+    const float Dl = ld(Dv + ld_d);
+    float d_cur[SPG], d_nxt[SPG], y_cur[SPG], y_nxt[SPG];
+    float dDl = 0.f;
     auto commit = [&](int k) {
         float vd[SPG], vdu[SPG], vu[SPG], vy[SPG];
         float vmax = 0.f;
@@ -418,6 +422,9 @@ ssm_bwd_kernel(
             }
             vdu[s] = vd[s] * vu[s];
             vmax = __builtin_fmaxf(vmax, __builtin_fabsf(vd[s]));
+            d_nxt[s] = vd[s];
+            y_nxt[s] = vy[s];
+            dDl = __builtin_fmaf(vy[s], vu[s], dDl);  // rows past L read as 0
         }
         if constexpr (XF) {
             if (zb != nullptr) {  // dz = dout * out * silu'(z) needs no scan: store it now
@@ -460,9 +467,11 @@ ssm_bwd_kernel(
     for (int k = k1 - 1; k >= k0; --k) {
         const int t0 = k * TC;
         const bool more = k > k0;
-        if constexpr (XF) {
 #pragma unroll
-            for (int s = 0; s < SPG; ++s) dd_cur[s] = dd_nxt[s];
+        for (int s = 0; s < SPG; ++s) {
+            d_cur[s] = d_nxt[s];
+            y_cur[s] = y_nxt[s];
+            if constexpr (XF) dd_cur[s] = dd_nxt[s];
         }
         if (more) issue(k - 1);
         // one workgroup-uniform decision per chunk: the clamped path gives the same values whenever
@@ -534,9 +543,13 @@ ssm_bwd_kernel(
         };
         {
             float uq[4], yq[4], dq[4], uqn[4], yqn[4], dqn[4], Bn[SPL], Cn[SPL];
-            // lane g keeps du/ddelta of the steps i with i % LPC == g and writes them after the sweep
-            constexpr int KPL = TC / LPC;
-            float kdu[KPL] = {}, kdd[KPL] = {};
+            // The group sums over n of each step, S1 = sum g*B (for du) and S2 = sum g*(A*dA*h_{t-1} +
+            // u*B) (= ddelta), are reduce-scattered over the group every RST steps: the lane's partials of
+            // RST steps x (S1, S2) go in, and the lane writes the one (step, sum) the scatter leaves it.
+            constexpr int RV = LPC, RST = RV / 2;
+            float rp[RV];
+            const int ridx = rs_index<RV>(lane);
+            float* const s_mine = &s_out[ridx & 1][ridx >> 1][c];  // + the round's first step * OS
             ldv<4>(s_in(2, c) + TC - 4, uqn);
             ldv<4>(s_in(3, c) + TC - 4, yqn);
             ldv<4>(s_in(0, c) + TC - 4, dqn);
@@ -591,18 +604,9 @@ ssm_bwd_kernel(
                     r2 = __builtin_fmaf(An[j], s, r2);
                     dAacc[j] = __builtin_fmaf(dti, s, dAacc[j]);
                 }
-                r1 = group_sum<LPC>(r1);
-                r2 = group_sum<LPC>(r2);
-                // every lane of the group holds the sums
-                {
-                    const float vdu = __builtin_fmaf(Dd, yo, dti * r1), vdd = __builtin_fmaf(ui, r1, r2);
-                    const bool mine = g == i % LPC;
-                    kdu[i / LPC] = mine ? vdu : kdu[i / LPC];
-                    kdd[i / LPC] = mine ? vdd : kdd[i / LPC];
-                    // select now: the two step values are dead after this step
-                    asm("" : "+v"(kdu[i / LPC]), "+v"(kdd[i / LPC]));
-                }
-                dDacc = __builtin_fmaf(yo, ui, dDacc);
+                rp[2 * (i % RST)] = r1;
+                rp[2 * (i % RST) + 1] = __builtin_fmaf(ui, r1, r2);
+                if (i % RST == 0) s_mine[i * OS] = reduce_scatter<LPC, RV>(rp, lane);
                 const int sl = slot * CPW + cw;
                 stv<SPL>(red_g + sl * NS + n0, gt);
                 stv<SPL>(red_h + sl * NS + n0, H[i]);
@@ -611,11 +615,6 @@ ssm_bwd_kernel(
                     fold(phase);
                     wave_lds_fence();
                 }
-            }
-#pragma unroll
-            for (int q = 0; q < KPL; ++q) {
-                s_out[0][q * LPC + g][c] = kdu[q];
-                s_out[1][q * LPC + g][c] = kdd[q];
             }
         }
         __syncthreads();  // every wave is done with the staged chunk and has written s_out / s_part
@@ -630,7 +629,8 @@ ssm_bwd_kernel(
             const rsrc_t rdd = make_rsrc(ddelta + rowD + (int64_t)t0 * D, chunk_rows(k) * row_bytes);
 #pragma unroll
             for (int s = 0; s < SPG; ++s) {
-                buf_st<T>(rdu, lofs + s * row_bytes, s_out[0][sg * SPG + s][lc]);
+                const float s1 = s_out[0][sg * SPG + s][lc];
+                buf_st<T>(rdu, lofs + s * row_bytes, __builtin_fmaf(Dl, y_cur[s], d_cur[s] * s1));
                 float dd = s_out[1][sg * SPG + s][lc];
                 if constexpr (XF) {
                     dd *= dd_cur[s];  // through softplus (1 without it)
@@ -655,19 +655,23 @@ ssm_bwd_kernel(
         }
         const int64_t pr = (int64_t)seg * Bsz + b;  // partial row
         stv<SPL>(dA_part + (pr * D + d) * NS + n0, dAacc);
-        if (g == 0) dD_part[pr * D + d] = dDacc;
     }
-    if constexpr (XF) {
-        if (xf.delta_bias != nullptr) {  // delta_bias partial: the NSG loader threads of a channel, in order
-            __syncthreads();
-            float* red = &s_out[0][0][0];  // free after the chunk loop; NSG*CPB <= 2*TC*OS floats
-            red[sg * CPB + lc] = dbias_acc;
-            __syncthreads();
-            if (tid < CPB && d0 + tid < D) {
-                float acc = 0.f;
-                for (int q = 0; q < NSG; ++q) acc += red[q * CPB + tid];
-                dbias_part[((int64_t)seg * Bsz + b) * D + d0 + tid] = acc;
+    {  // dD (and delta_bias) partials: the NSG loader threads of a channel, in order
+        const bool with_bias = XF && xf.delta_bias != nullptr;
+        __syncthreads();
+        float* red = &s_out[0][0][0];  // free after the chunk loop; 2*NSG*CPB <= 2*TC*OS floats
+        red[sg * CPB + lc] = dDl;
+        if (with_bias) red[NSG * CPB + sg * CPB + lc] = dbias_acc;
+        __syncthreads();
+        if (tid < CPB && d0 + tid < D) {
+            const int64_t pr = (int64_t)seg * Bsz + b;
+            float acc = 0.f, accb = 0.f;
+            for (int q = 0; q < NSG; ++q) {
+                acc += red[q * CPB + tid];
+                if (with_bias) accb += red[NSG * CPB + q * CPB + tid];
             }
+            dD_part[pr * D + d0 + tid] = acc;
+            if (with_bias) dbias_part[pr * D + d0 + tid] = accb;
         }
     }
 }

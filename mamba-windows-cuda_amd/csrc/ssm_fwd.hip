@@ -267,9 +267,11 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
 #pragma unroll
         for (int i = 0; i < TC; ++i) dmax = __builtin_fmaxf(dmax, __builtin_fabsf(dt[i]));
         const bool need_clamp = __builtin_amdgcn_ballot_w64(dmax * amax2 > kExp2Clamp) != 0;
-        // lane g keeps y of the steps i with i % LPC == g and writes them after the chunk
-        constexpr int KPL = TC / LPC;
-        float ky[KPL] = {};
+        // the lane partials of y are reduce-scattered over the group every RV steps; the lane writes
+        // the step's y the scatter leaves it (each step is held by two lanes of the group)
+        constexpr int RV = LPC / 2;
+        float ry[RV];
+        float* const y_mine = &s_y[HAS_OUT ? buf : 0][HAS_OUT ? rs_index<RV>(lane) : 0][HAS_OUT ? c : 0];
         auto run = [&](auto clamp_tag) {
             constexpr bool CLAMP = decltype(clamp_tag)::value;
 #pragma unroll
@@ -286,10 +288,8 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
                     if constexpr (HAS_OUT) y = __builtin_fmaf(Cv[i][j], h[j], y);
                 }
                 if constexpr (HAS_OUT) {
-                    // every lane of the group holds the sum
-                    const float ys = group_sum<LPC>(y);
-                    ky[i / LPC] = g == i % LPC ? ys : ky[i / LPC];
-                    asm("" : "+v"(ky[i / LPC]));  // select now: ys is dead after this step
+                    ry[i % RV] = y;
+                    if (i % RV == RV - 1) y_mine[(i - (RV - 1)) * YS] = reduce_scatter<LPC, RV>(ry, lane);
                 }
             }
         };
@@ -304,10 +304,6 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
 #pragma unroll
                 for (int j = 0; j < SPL; ++j) xs[j] = __builtin_fmaf(A2[j], sdt, xs[j]);
             }
-        }
-        if constexpr (HAS_OUT) {
-#pragma unroll
-            for (int q = 0; q < KPL; ++q) s_y[buf][q * LPC + g][c] = ky[q];
         }
         if (more) commit(k + 1, buf ^ 1);
         __syncthreads();
