@@ -112,6 +112,8 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
 
     __shared__ __align__(16) float s_in[2][2][CPB][RS];  // [buf][delta, dout][channel][step]
     __shared__ __align__(16) float s_c[2][TC][NS];
+    // per staging buffer: the index of the last chunk staged there whose exponents can reach the clamp
+    __shared__ int s_flag[2];
 
     const int tid = threadIdx.x;
     const int lid = xcd_remap(blockIdx.x, gridDim.x);
@@ -133,14 +135,17 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
     const int64_t row0 = (int64_t)b * L;
 
     float A2[SPL], gc[SPL], xs[SPL];
-    float amax2 = 0.f;
 #pragma unroll
     for (int j = 0; j < SPL; ++j) {
         A2[j] = ld(A + (int64_t)d * NS + n0 + j) * kLog2e;
-        amax2 = __builtin_fmaxf(amax2, __builtin_fabsf(A2[j]));
         gc[j] = 0.f;
-        xs[j] = 0.f;
+        xs[j] = 0.f;  // the clamped exponents' departure from A2 * sum(delta)
     }
+    float lamax2 = 0.f;  // max_n |A[ld_d][n]| * log2(e): the loader flags chunks that reach the clamp
+#pragma unroll
+    for (int n = 0; n < NS; ++n) lamax2 = __builtin_fmaxf(lamax2, __builtin_fabsf(ld(A + (int64_t)ld_d * NS + n)));
+    lamax2 *= kLog2e;
+    float sdt_l = 0.f;  // the sum of the loader's delta values over the carry segment
 
     // buffer resources per chunk: rows past L and channels past D read as 0 (see the main kernel)
     const uint32_t lofs = lvalid ? ((uint32_t)(sg * SPG) * (uint32_t)D + (uint32_t)ld_d) * sizeof(T) : kOob;
@@ -170,6 +175,7 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
     };
     auto commit = [&](int k, int buf) {
         float vd[SPG], vy[SPG];
+        float vmax = 0.f;
 #pragma unroll
         for (int s = 0; s < SPG; ++s) {
             vd[s] = static_cast<float>(pd[s]);
@@ -185,7 +191,10 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
                     vy[s] *= zv * sigmoid_f(zv);
                 }
             }
+            vmax = __builtin_fmaxf(vmax, __builtin_fabsf(vd[s]));
+            sdt_l += vd[s];
         }
+        if (vmax * lamax2 > kExp2Clamp) s_flag[buf] = k;  // benign race: every writer stores k
         stv<SPG>(&s_in[buf][0][lc][sg * SPG], vd);
         stv<SPG>(&s_in[buf][1][lc][sg * SPG], vy);
 #pragma unroll
@@ -195,6 +204,8 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
         }
     };
 
+    if (tid < 2) s_flag[tid] = -1;
+    __syncthreads();
     if (k0 < k1) {
         issue(k1 - 1);
         commit(k1 - 1, (k1 - 1) & 1);
@@ -209,10 +220,8 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
         ldv<TC>(&s_in[buf][1][c][0], yo);
 #pragma unroll
         for (int i = 0; i < TC; ++i) ldv<SPL>(&s_c[buf][i][n0], Cv[i]);
-        float dmax = 0.f;
-#pragma unroll
-        for (int i = 0; i < TC; ++i) dmax = __builtin_fmaxf(dmax, __builtin_fabsf(dt[i]));
-        const bool need_clamp = __builtin_amdgcn_ballot_w64(dmax * amax2 > kExp2Clamp) != 0;
+        // one workgroup-uniform decision per chunk (exact: see the main kernel)
+        const bool need_clamp = __builtin_amdgcn_readfirstlane(s_flag[buf]) == k;
         auto run = [&](auto clamp_tag) {
             constexpr bool CLAMP = decltype(clamp_tag)::value;
 #pragma unroll
@@ -221,25 +230,29 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
                 for (int j = 0; j < SPL; ++j) {
                     float x = dt[i] * A2[j];
                     if constexpr (CLAMP) {
-                        x = __builtin_fminf(__builtin_fmaxf(x, -kExp2Clamp), kExp2Clamp);
-                        xs[j] += x;
+                        const float xc = __builtin_fminf(__builtin_fmaxf(x, -kExp2Clamp), kExp2Clamp);
+                        xs[j] += xc - x;  // the clamp's share of the exponent sum
+                        x = xc;
                     }
                     gc[j] = __builtin_amdgcn_exp2f(x) * __builtin_fmaf(yo[i], Cv[i][j], gc[j]);
                 }
             }
         };
-        if (need_clamp) {
+        if (need_clamp)
             run(std::true_type{});
-        } else {
+        else
             run(std::false_type{});
-            float sdt = 0.f;
-#pragma unroll
-            for (int i = 0; i < TC; ++i) sdt += dt[i];
-#pragma unroll
-            for (int j = 0; j < SPL; ++j) xs[j] = __builtin_fmaf(A2[j], sdt, xs[j]);
-        }
         if (more) commit(k - 1, buf ^ 1);
         __syncthreads();
+    }
+    {  // summed exponent: A2 * (the channel's delta summed by its NSG loader threads), plus the clamp's share
+        float* red = &s_in[0][0][0][0];  // free after the chunk loop; NSG*CPB = 256 floats
+        red[sg * CPB + lc] = sdt_l;
+        __syncthreads();
+        float sdt = 0.f;
+        for (int q = 0; q < NSG; ++q) sdt += red[q * CPB + c];
+#pragma unroll
+        for (int j = 0; j < SPL; ++j) xs[j] = __builtin_fmaf(A2[j], sdt, xs[j]);
     }
     if (valid) {
         const int64_t o = (((int64_t)b * ncar + seg) * D + d) * NS + n0;

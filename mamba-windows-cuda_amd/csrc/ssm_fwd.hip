@@ -101,6 +101,8 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
     // ([step][n / SPL][B x SPL, C x SPL]) so a lane reads both with one 2*SPL-float access
     __shared__ __align__(16) float s_bc[2][TC][HAS_OUT ? 2 * NS : NS];
     __shared__ __align__(16) float s_y[HAS_OUT ? 2 : 1][HAS_OUT ? TC : 1][HAS_OUT ? YS : 1];
+    // per staging buffer: the index of the last chunk staged there whose exponents can reach the clamp
+    __shared__ int s_flag[2];
 
     const int tid = threadIdx.x;
     const int lid = xcd_remap(blockIdx.x, gridDim.x);
@@ -129,14 +131,18 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
     const int64_t car_seg = (int64_t)D * NS;
 
     float A2[SPL], h[SPL], xs[SPL];
-    float amax2 = 0.f;  // max_j |A_j| * log2(e) over this lane's states
 #pragma unroll
     for (int j = 0; j < SPL; ++j) {
         A2[j] = ld(A + (int64_t)d * NS + n0 + j) * kLog2e;
-        amax2 = __builtin_fmaxf(amax2, __builtin_fabsf(A2[j]));
         h[j] = (!CARRY && h_prev) ? ld(h_prev + ((int64_t)b * D + d) * NS + n0 + j) : 0.f;
-        xs[j] = 0.f;
+        xs[j] = 0.f;  // carry: the clamped exponents' departure from A2 * sum(delta)
     }
+    // max_n |A[ld_d][n]| * log2(e): the loader flags the chunks whose exponents can reach the clamp
+    float lamax2 = 0.f;
+#pragma unroll
+    for (int n = 0; n < NS; ++n) lamax2 = __builtin_fmaxf(lamax2, __builtin_fabsf(ld(A + (int64_t)ld_d * NS + n)));
+    lamax2 *= kLog2e;
+    float sdt_l = 0.f;  // carry: the sum of the loader's delta values over the segment
     if constexpr (!CARRY) {
 #pragma unroll 4
         for (int j = 0; j < seg * cfold; ++j) {  // h -> 2^xsum * h + h_end of each preceding carry segment
@@ -191,6 +197,7 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
     float du_cur[SPG], du_nxt[SPG], gz_cur[SPG], gz_nxt[SPG];
     auto commit = [&](int k, int buf) {
         float vd[SPG], vdu[SPG];
+        float vmax = 0.f;
 #pragma unroll
         for (int s = 0; s < SPG; ++s) {
             vd[s] = static_cast<float>(pd[s]);
@@ -199,6 +206,8 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
                 if (xf.softplus) vd[s] = softplus_f(vd[s]);
                 if (k * TC + sg * SPG + s >= L) vd[s] = 0.f;
             }
+            vmax = __builtin_fmaxf(vmax, __builtin_fabsf(vd[s]));
+            if constexpr (CARRY) sdt_l += vd[s];
             const float vu = static_cast<float>(pu[s]);
             vdu[s] = vd[s] * vu;
             du_nxt[s] = Dl * vu;
@@ -207,6 +216,7 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
                 gz_nxt[s] = zv * sigmoid_f(zv);  // silu(z)
             }
         }
+        if (vmax * lamax2 > kExp2Clamp) s_flag[buf] = k;  // benign race: every writer stores k
         vst<SPG>(&s_in[buf][0][lc][sg * SPG], vd);
         vst<SPG>(&s_in[buf][1][lc][sg * SPG], vdu);
 #pragma unroll
@@ -225,6 +235,8 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
         }
     };
 
+    if (tid < 2) s_flag[tid] = -1;
+    __syncthreads();
     if (k0 < k1) {  // every segment holds a chunk unless L == 0 (then h_last = h_prev)
         issue(k0);
         commit(k0, k0 & 1);
@@ -262,11 +274,10 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
                 lds_ld<SPL>(&s_bc[buf][i][n0], Bv[i]);
             }
         }
-        // |delta*A| <= 88 for the whole chunk (the usual case) -> no clamp needed
-        float dmax = 0.f;
-#pragma unroll
-        for (int i = 0; i < TC; ++i) dmax = __builtin_fmaxf(dmax, __builtin_fabsf(dt[i]));
-        const bool need_clamp = __builtin_amdgcn_ballot_w64(dmax * amax2 > kExp2Clamp) != 0;
+        // one workgroup-uniform decision per chunk: the loaders flag a chunk in which some |delta*A|
+        // can exceed 88; the clamped path gives the same values whenever none does, so deciding for the
+        // whole workgroup is exact
+        const bool need_clamp = __builtin_amdgcn_readfirstlane(s_flag[buf]) == k;
         // the lane partials of y are reduce-scattered over the group every RV steps; the lane writes
         // the step's y the scatter leaves it (each step is held by two lanes of the group)
         constexpr int RV = LPC / 2;
@@ -281,8 +292,9 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
                 for (int j = 0; j < SPL; ++j) {
                     float x = dt[i] * A2[j];
                     if constexpr (CLAMP) {
-                        x = __builtin_fminf(__builtin_fmaxf(x, -kExp2Clamp), kExp2Clamp);
-                        if constexpr (CARRY) xs[j] += x;
+                        const float xc = __builtin_fminf(__builtin_fmaxf(x, -kExp2Clamp), kExp2Clamp);
+                        if constexpr (CARRY) xs[j] += xc - x;  // the clamp's share of the exponent sum
+                        x = xc;
                     }
                     h[j] = __builtin_fmaf(__builtin_amdgcn_exp2f(x), h[j], dtu[i] * Bv[i][j]);
                     if constexpr (HAS_OUT) y = __builtin_fmaf(Cv[i][j], h[j], y);
@@ -293,18 +305,10 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
                 }
             }
         };
-        if (need_clamp) {
+        if (need_clamp)
             run(std::true_type{});
-        } else {
+        else
             run(std::false_type{});
-            if constexpr (CARRY) {
-                float sdt = 0.f;
-#pragma unroll
-                for (int i = 0; i < TC; ++i) sdt += dt[i];
-#pragma unroll
-                for (int j = 0; j < SPL; ++j) xs[j] = __builtin_fmaf(A2[j], sdt, xs[j]);
-            }
-        }
         if (more) commit(k + 1, buf ^ 1);
         __syncthreads();
         if constexpr (HAS_OUT) {
@@ -321,6 +325,15 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
         }
     }
     if constexpr (CARRY) {
+        // summed exponent of each state: A2 * (the channel's delta summed by its NSG loader threads),
+        // plus the clamp's share
+        float* red = &s_in[0][0][0][0];  // free after the chunk loop; NSG*CPB = 256 floats
+        red[sg * CPB + lc] = sdt_l;
+        __syncthreads();
+        float sdt = 0.f;
+        for (int q = 0; q < NSG; ++q) sdt += red[q * CPB + c];
+#pragma unroll
+        for (int j = 0; j < SPL; ++j) xs[j] = __builtin_fmaf(A2[j], sdt, xs[j]);
         if (valid) {
             vst<SPL>(car_h + car0 + seg * car_seg, h);
             vst<SPL>(car_x + car0 + seg * car_seg, xs);
