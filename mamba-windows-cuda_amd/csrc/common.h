@@ -115,46 +115,180 @@ template <int G> __device__ __forceinline__ float group_sum(float v) {
 }
 
 // Reduce-scatter over aligned groups of G lanes (G in {2,4,8,16}) of V values per lane (V a power of
-// two, 2 <= V <= G): the lane returns the group sum of value rs_index<V>(lane); each index is held by
-// G/V lanes of the group. Level l pairs a lane with its DPP partner of group_sum (xor 1, xor 2, mirror
-// in 8, mirror in 16). At the first log2(V) levels the pair splits its values by a lane bit b_l that
-// differs between the partners and agrees on every lower level's bit -- b0 = i0^i2, b1 = i1^i2,
-// b2 = i2^i3, b3 = i3 for lane i of a 16-lane row -- each keeping one half and adding the partner's
-// copy of it (two selects and one DPP add per pair, against one DPP add per value and level for V
-// separate group sums); the remaining levels add the single value.
-__device__ __forceinline__ int rs_bit(int level, int lane) {
-    const int x = lane & 15;
-    const int i2 = (x >> 2) & 1, i3 = (x >> 3) & 1;
-    return level == 0 ? ((x & 1) ^ i2) : level == 1 ? (((x >> 1) & 1) ^ i2) : level == 2 ? (i2 ^ i3) : i3;
+// two, 2 <= V <= G): the lane returns the group sum of value rs_index<G, V>(lane); each index is held
+// by G/V lanes of the group. The levels pair a lane with its DPP partner, first across the 4-lane
+// banks of the 16-lane row (mirror in 16, then mirror in 8), then inside a bank (xor 2, xor 1). At the
+// first log2(V) levels the pair splits its values by a lane bit that differs between the partners and
+// agrees on every earlier level's bit -- i3, i2, i1, i0 of the lane's index i in its row, in that
+// level order -- each lane keeping one half and adding the partner's copy of it; the remaining levels
+// add the single value. Across banks the bit is a function of the bank, so one DPP add per half, each
+// enabled on the banks that keep that half, does a pair in two instructions; inside a bank it takes
+// two selects and one DPP add.
+template <int G> __device__ __forceinline__ int rs_bit(int level, int lane) {
+    // level order: mirror in 16 (G = 16 only), mirror in 8 (G >= 8), xor 2 (G >= 4), xor 1
+    constexpr int first = G >= 16 ? 3 : G >= 8 ? 2 : G >= 4 ? 1 : 0;  // lane bit of level 0
+    return (lane >> (first - level)) & 1;
 }
-template <int V> __device__ __forceinline__ int rs_index(int lane) {
+template <int G, int V> __device__ __forceinline__ int rs_index(int lane) {
     int idx = 0;
 #pragma unroll
-    for (int l = 0; (1 << l) < V; ++l) idx |= rs_bit(l, lane) << l;
+    for (int l = 0; (1 << l) < V; ++l) idx |= rs_bit<G>(l, lane) << l;
     return idx;
 }
-template <int L> __device__ __forceinline__ float dpp_level(float v) {
-    if constexpr (L == 0) return dpp<kDppXor1>(v);
-    if constexpr (L == 1) return dpp<kDppXor2>(v);
-    if constexpr (L == 2) return dpp<kDppHalfMirror>(v);
-    if constexpr (L == 3) return dpp<kDppMirror>(v);
+// The partner's copy of v at the level whose partner flips lane bits 0..b (b = 3: mirror in 16,
+// b = 2: mirror in 8, b = 1: xor 2, b = 0: xor 1).
+template <int B> __device__ __forceinline__ float dpp_flip(float v) {
+    if constexpr (B == 3) return dpp<kDppMirror>(v);
+    if constexpr (B == 2) return dpp<kDppHalfMirror>(v);
+    if constexpr (B == 1) return dpp<kDppXor2>(v);
+    if constexpr (B == 0) return dpp<kDppXor1>(v);
+}
+// One cross-bank level of the reduce-scatter on NP value pairs: lanes whose bank keeps half 0 get
+// x[2q] + the partner's x[2q], the others x[2q+1] + the partner's x[2q+1]. B = 3: mirror in 16, lane bit
+// i3 (banks 0,1 keep half 0); B = 2: mirror in 8, lane bit i2 (banks 0,2). Each pair is two DPP adds,
+// each enabled on the banks that keep its half. The leading s_nop gives the two wait states a DPP read
+// needs after a VALU write of its source; the trailing one covers a DPP read of the results after the
+// block (the compiler does not look inside it).
+template <int B, int NP> __device__ __forceinline__ void dpp_bank_level(const float* x, float* r) {
+    static_assert(B == 2 || B == 3, "cross-bank levels only");
+    if constexpr (B == 3) {
+        if constexpr (NP == 1) {
+            asm("s_nop 1\n\t"
+            "v_add_f32_dpp %0, %1, %1 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+            "v_add_f32_dpp %0, %2, %2 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+            "s_nop 1"
+            : "=&v"(r[0])
+            : "v"(x[0]), "v"(x[1]));
+        }
+        else if constexpr (NP == 2) {
+            asm("s_nop 1\n\t"
+            "v_add_f32_dpp %0, %2, %2 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+            "v_add_f32_dpp %0, %3, %3 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+            "v_add_f32_dpp %1, %4, %4 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+            "v_add_f32_dpp %1, %5, %5 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+            "s_nop 1"
+            : "=&v"(r[0]), "=&v"(r[1])
+            : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]));
+        }
+        else if constexpr (NP == 4) {
+            asm("s_nop 1\n\t"
+            "v_add_f32_dpp %0, %4, %4 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+            "v_add_f32_dpp %0, %5, %5 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+            "v_add_f32_dpp %1, %6, %6 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+            "v_add_f32_dpp %1, %7, %7 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+            "v_add_f32_dpp %2, %8, %8 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+            "v_add_f32_dpp %2, %9, %9 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+            "v_add_f32_dpp %3, %10, %10 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+            "v_add_f32_dpp %3, %11, %11 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+            "s_nop 1"
+            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+            : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]), "v"(x[5]), "v"(x[6]), "v"(x[7]));
+        }
+        else if constexpr (NP == 8) {
+            asm("s_nop 1\n\t"
+            "v_add_f32_dpp %0, %8, %8 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+            "v_add_f32_dpp %0, %9, %9 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+            "v_add_f32_dpp %1, %10, %10 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+            "v_add_f32_dpp %1, %11, %11 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+            "v_add_f32_dpp %2, %12, %12 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+            "v_add_f32_dpp %2, %13, %13 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+            "v_add_f32_dpp %3, %14, %14 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+            "v_add_f32_dpp %3, %15, %15 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+            "v_add_f32_dpp %4, %16, %16 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+            "v_add_f32_dpp %4, %17, %17 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+            "v_add_f32_dpp %5, %18, %18 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+            "v_add_f32_dpp %5, %19, %19 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+            "v_add_f32_dpp %6, %20, %20 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+            "v_add_f32_dpp %6, %21, %21 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+            "v_add_f32_dpp %7, %22, %22 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+            "v_add_f32_dpp %7, %23, %23 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+            "s_nop 1"
+            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
+            : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]), "v"(x[5]), "v"(x[6]), "v"(x[7]), "v"(x[8]), "v"(x[9]), "v"(x[10]), "v"(x[11]), "v"(x[12]), "v"(x[13]), "v"(x[14]), "v"(x[15]));
+        }
+    }
+    if constexpr (B == 2) {
+        if constexpr (NP == 1) {
+            asm("s_nop 1\n\t"
+            "v_add_f32_dpp %0, %1, %1 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+            "v_add_f32_dpp %0, %2, %2 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+            "s_nop 1"
+            : "=&v"(r[0])
+            : "v"(x[0]), "v"(x[1]));
+        }
+        else if constexpr (NP == 2) {
+            asm("s_nop 1\n\t"
+            "v_add_f32_dpp %0, %2, %2 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+            "v_add_f32_dpp %0, %3, %3 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+            "v_add_f32_dpp %1, %4, %4 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+            "v_add_f32_dpp %1, %5, %5 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+            "s_nop 1"
+            : "=&v"(r[0]), "=&v"(r[1])
+            : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]));
+        }
+        else if constexpr (NP == 4) {
+            asm("s_nop 1\n\t"
+            "v_add_f32_dpp %0, %4, %4 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+            "v_add_f32_dpp %0, %5, %5 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+            "v_add_f32_dpp %1, %6, %6 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+            "v_add_f32_dpp %1, %7, %7 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+            "v_add_f32_dpp %2, %8, %8 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+            "v_add_f32_dpp %2, %9, %9 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+            "v_add_f32_dpp %3, %10, %10 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+            "v_add_f32_dpp %3, %11, %11 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+            "s_nop 1"
+            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+            : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]), "v"(x[5]), "v"(x[6]), "v"(x[7]));
+        }
+        else if constexpr (NP == 8) {
+            asm("s_nop 1\n\t"
+            "v_add_f32_dpp %0, %8, %8 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+            "v_add_f32_dpp %0, %9, %9 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+            "v_add_f32_dpp %1, %10, %10 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+            "v_add_f32_dpp %1, %11, %11 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+            "v_add_f32_dpp %2, %12, %12 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+            "v_add_f32_dpp %2, %13, %13 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+            "v_add_f32_dpp %3, %14, %14 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+            "v_add_f32_dpp %3, %15, %15 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+            "v_add_f32_dpp %4, %16, %16 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+            "v_add_f32_dpp %4, %17, %17 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+            "v_add_f32_dpp %5, %18, %18 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+            "v_add_f32_dpp %5, %19, %19 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+            "v_add_f32_dpp %6, %20, %20 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+            "v_add_f32_dpp %6, %21, %21 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+            "v_add_f32_dpp %7, %22, %22 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+            "v_add_f32_dpp %7, %23, %23 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+            "s_nop 1"
+            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
+            : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]), "v"(x[5]), "v"(x[6]), "v"(x[7]), "v"(x[8]), "v"(x[9]), "v"(x[10]), "v"(x[11]), "v"(x[12]), "v"(x[13]), "v"(x[14]), "v"(x[15]));
+        }
+    }
 }
 template <int G, int V, int L = 0, int M = V>
 __device__ __forceinline__ float reduce_scatter_lv(float (&x)[V], int lane) {
     static_assert(V >= 2 && V <= G && (V & (V - 1)) == 0 && (G & (G - 1)) == 0 && G <= 16, "shape");
-    if constexpr ((1 << L) >= G) {
+    constexpr int first = G >= 16 ? 3 : G >= 8 ? 2 : G >= 4 ? 1 : 0;
+    constexpr int B = first - L;  // lane bit (and partner) of this level
+    if constexpr (B < 0) {
         return x[0];
     } else if constexpr (M > 1) {
-        const bool hi = rs_bit(L, lane) != 0;
+        if constexpr (B >= 2) {
+            float r[M / 2];
+            dpp_bank_level<B, M / 2>(x, r);
 #pragma unroll
-        for (int q = 0; q < M / 2; ++q) {
-            const float keep = hi ? x[2 * q + 1] : x[2 * q];
-            const float send = hi ? x[2 * q] : x[2 * q + 1];
-            x[q] = keep + dpp_level<L>(send);
+            for (int q = 0; q < M / 2; ++q) x[q] = r[q];
+        } else {
+            const bool hi = rs_bit<G>(L, lane) != 0;
+#pragma unroll
+            for (int q = 0; q < M / 2; ++q) {
+                const float keep = hi ? x[2 * q + 1] : x[2 * q];
+                const float send = hi ? x[2 * q] : x[2 * q + 1];
+                x[q] = keep + dpp_flip<B>(send);
+            }
         }
         return reduce_scatter_lv<G, V, L + 1, M / 2>(x, lane);
     } else {
-        x[0] += dpp_level<L>(x[0]);
+        x[0] += dpp_flip<B>(x[0]);
         return reduce_scatter_lv<G, V, L + 1, 1>(x, lane);
     }
 }

@@ -551,6 +551,8 @@ ssm_bwd_kernel(
                     if constexpr (LPI >= 2) acc[q] += dpp<kDppXor1>(acc[q]);
                     if constexpr (LPI >= 4) acc[q] += dpp<kDppXor2>(acc[q]);
                 }
+                // combine in every lane, ahead of the store's lane mask, so each DPP move fuses into its add
+                asm("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]));
                 if (rsub == 0) stv<4>(&s_part[wave][phase * kRedSlots + rs][rq * 4], acc);
             }
         };
@@ -561,7 +563,7 @@ ssm_bwd_kernel(
             // RST steps x (S1, S2) go in, and the lane writes the one (step, sum) the scatter leaves it.
             constexpr int RV = LPC, RST = RV / 2;
             float rp[RV];
-            const int ridx = rs_index<RV>(lane);
+            const int ridx = rs_index<LPC, RV>(lane);
             float* const s_mine = &s_out[ridx & 1][ridx >> 1][c];  // + the round's first step * OS
             ldv<4>(s_in(2, c) + TC - 4, uqn);
             ldv<4>(s_in(3, c) + TC - 4, yqn);

@@ -282,7 +282,7 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
         // the step's y the scatter leaves it (each step is held by two lanes of the group)
         constexpr int RV = LPC / 2;
         float ry[RV];
-        float* const y_mine = &s_y[HAS_OUT ? buf : 0][HAS_OUT ? rs_index<RV>(lane) : 0][HAS_OUT ? c : 0];
+        float* const y_mine = &s_y[HAS_OUT ? buf : 0][HAS_OUT ? rs_index<LPC, RV>(lane) : 0][HAS_OUT ? c : 0];
         auto run = [&](auto clamp_tag) {
             constexpr bool CLAMP = decltype(clamp_tag)::value;
 #pragma unroll
