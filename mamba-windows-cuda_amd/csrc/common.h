@@ -149,121 +149,45 @@ template <int B> __device__ __forceinline__ float dpp_flip(float v) {
 // each enabled on the banks that keep its half. The leading s_nop gives the two wait states a DPP read
 // needs after a VALU write of its source; the trailing one covers a DPP read of the results after the
 // block (the compiler does not look inside it).
-template <int B, int NP> __device__ __forceinline__ void dpp_bank_level(const float* x, float* r) {
-    static_assert(B == 2 || B == 3, "cross-bank levels only");
-    if constexpr (B == 3) {
-        if constexpr (NP == 1) {
-            asm("s_nop 1\n\t"
-            "v_add_f32_dpp %0, %1, %1 row_mirror row_mask:0xf bank_mask:0x3\n\t"
-            "v_add_f32_dpp %0, %2, %2 row_mirror row_mask:0xf bank_mask:0xc\n\t"
-            "s_nop 1"
-            : "=&v"(r[0])
-            : "v"(x[0]), "v"(x[1]));
-        }
-        else if constexpr (NP == 2) {
-            asm("s_nop 1\n\t"
-            "v_add_f32_dpp %0, %2, %2 row_mirror row_mask:0xf bank_mask:0x3\n\t"
-            "v_add_f32_dpp %0, %3, %3 row_mirror row_mask:0xf bank_mask:0xc\n\t"
-            "v_add_f32_dpp %1, %4, %4 row_mirror row_mask:0xf bank_mask:0x3\n\t"
-            "v_add_f32_dpp %1, %5, %5 row_mirror row_mask:0xf bank_mask:0xc\n\t"
-            "s_nop 1"
-            : "=&v"(r[0]), "=&v"(r[1])
-            : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]));
-        }
-        else if constexpr (NP == 4) {
-            asm("s_nop 1\n\t"
-            "v_add_f32_dpp %0, %4, %4 row_mirror row_mask:0xf bank_mask:0x3\n\t"
-            "v_add_f32_dpp %0, %5, %5 row_mirror row_mask:0xf bank_mask:0xc\n\t"
-            "v_add_f32_dpp %1, %6, %6 row_mirror row_mask:0xf bank_mask:0x3\n\t"
-            "v_add_f32_dpp %1, %7, %7 row_mirror row_mask:0xf bank_mask:0xc\n\t"
-            "v_add_f32_dpp %2, %8, %8 row_mirror row_mask:0xf bank_mask:0x3\n\t"
-            "v_add_f32_dpp %2, %9, %9 row_mirror row_mask:0xf bank_mask:0xc\n\t"
-            "v_add_f32_dpp %3, %10, %10 row_mirror row_mask:0xf bank_mask:0x3\n\t"
-            "v_add_f32_dpp %3, %11, %11 row_mirror row_mask:0xf bank_mask:0xc\n\t"
-            "s_nop 1"
-            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
-            : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]), "v"(x[5]), "v"(x[6]), "v"(x[7]));
-        }
-        else if constexpr (NP == 8) {
-            asm("s_nop 1\n\t"
-            "v_add_f32_dpp %0, %8, %8 row_mirror row_mask:0xf bank_mask:0x3\n\t"
-            "v_add_f32_dpp %0, %9, %9 row_mirror row_mask:0xf bank_mask:0xc\n\t"
-            "v_add_f32_dpp %1, %10, %10 row_mirror row_mask:0xf bank_mask:0x3\n\t"
-            "v_add_f32_dpp %1, %11, %11 row_mirror row_mask:0xf bank_mask:0xc\n\t"
-            "v_add_f32_dpp %2, %12, %12 row_mirror row_mask:0xf bank_mask:0x3\n\t"
-            "v_add_f32_dpp %2, %13, %13 row_mirror row_mask:0xf bank_mask:0xc\n\t"
-            "v_add_f32_dpp %3, %14, %14 row_mirror row_mask:0xf bank_mask:0x3\n\t"
-            "v_add_f32_dpp %3, %15, %15 row_mirror row_mask:0xf bank_mask:0xc\n\t"
-            "v_add_f32_dpp %4, %16, %16 row_mirror row_mask:0xf bank_mask:0x3\n\t"
-            "v_add_f32_dpp %4, %17, %17 row_mirror row_mask:0xf bank_mask:0xc\n\t"
-            "v_add_f32_dpp %5, %18, %18 row_mirror row_mask:0xf bank_mask:0x3\n\t"
-            "v_add_f32_dpp %5, %19, %19 row_mirror row_mask:0xf bank_mask:0xc\n\t"
-            "v_add_f32_dpp %6, %20, %20 row_mirror row_mask:0xf bank_mask:0x3\n\t"
-            "v_add_f32_dpp %6, %21, %21 row_mirror row_mask:0xf bank_mask:0xc\n\t"
-            "v_add_f32_dpp %7, %22, %22 row_mirror row_mask:0xf bank_mask:0x3\n\t"
-            "v_add_f32_dpp %7, %23, %23 row_mirror row_mask:0xf bank_mask:0xc\n\t"
-            "s_nop 1"
-            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
-            : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]), "v"(x[5]), "v"(x[6]), "v"(x[7]), "v"(x[8]), "v"(x[9]), "v"(x[10]), "v"(x[11]), "v"(x[12]), "v"(x[13]), "v"(x[14]), "v"(x[15]));
-        }
+template <int B, int NP> __device__ __forceinline__ void dpp_bank_level(const float* x, float* r);
+
+// DPP controls and bank masks (half 0, half 1) of the two cross-bank levels
+#define MWC_BANK_ADD(o, i0, i1, ctrl, m0, m1)                                   \
+    "v_add_f32_dpp %" #o ", %" #i0 ", %" #i0 " " ctrl " row_mask:0xf bank_mask:" m0 "\n\t" \
+    "v_add_f32_dpp %" #o ", %" #i1 ", %" #i1 " " ctrl " row_mask:0xf bank_mask:" m1 "\n\t"
+#define MWC_BANK_LEVEL(B, CTRL, M0, M1)                                                                    \
+    template <> __device__ __forceinline__ void dpp_bank_level<B, 1>(const float* x, float* r) {            \
+        asm("s_nop 1\n\t" MWC_BANK_ADD(0, 1, 2, CTRL, M0, M1) "s_nop 1"                                      \
+            : "=&v"(r[0])                                                                                  \
+            : "v"(x[0]), "v"(x[1]));                                                                       \
+    }                                                                                                      \
+    template <> __device__ __forceinline__ void dpp_bank_level<B, 2>(const float* x, float* r) {            \
+        asm("s_nop 1\n\t" MWC_BANK_ADD(0, 2, 3, CTRL, M0, M1) MWC_BANK_ADD(1, 4, 5, CTRL, M0, M1) "s_nop 1"   \
+            : "=&v"(r[0]), "=&v"(r[1])                                                                     \
+            : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]));                                                 \
+    }                                                                                                      \
+    template <> __device__ __forceinline__ void dpp_bank_level<B, 4>(const float* x, float* r) {            \
+        asm("s_nop 1\n\t" MWC_BANK_ADD(0, 4, 5, CTRL, M0, M1) MWC_BANK_ADD(1, 6, 7, CTRL, M0, M1)           \
+                MWC_BANK_ADD(2, 8, 9, CTRL, M0, M1) MWC_BANK_ADD(3, 10, 11, CTRL, M0, M1) "s_nop 1"          \
+            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])                                           \
+            : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]), "v"(x[5]), "v"(x[6]), "v"(x[7]));     \
+    }                                                                                                      \
+    template <> __device__ __forceinline__ void dpp_bank_level<B, 8>(const float* x, float* r) {            \
+        asm("s_nop 1\n\t" MWC_BANK_ADD(0, 8, 9, CTRL, M0, M1) MWC_BANK_ADD(1, 10, 11, CTRL, M0, M1)         \
+                MWC_BANK_ADD(2, 12, 13, CTRL, M0, M1) MWC_BANK_ADD(3, 14, 15, CTRL, M0, M1)                  \
+                MWC_BANK_ADD(4, 16, 17, CTRL, M0, M1) MWC_BANK_ADD(5, 18, 19, CTRL, M0, M1)                  \
+                MWC_BANK_ADD(6, 20, 21, CTRL, M0, M1) MWC_BANK_ADD(7, 22, 23, CTRL, M0, M1) "s_nop 1"        \
+            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]),   \
+              "=&v"(r[7])                                                                                  \
+            : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]), "v"(x[5]), "v"(x[6]), "v"(x[7]),      \
+              "v"(x[8]), "v"(x[9]), "v"(x[10]), "v"(x[11]), "v"(x[12]), "v"(x[13]), "v"(x[14]),            \
+              "v"(x[15]));                                                                                 \
     }
-    if constexpr (B == 2) {
-        if constexpr (NP == 1) {
-            asm("s_nop 1\n\t"
-            "v_add_f32_dpp %0, %1, %1 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
-            "v_add_f32_dpp %0, %2, %2 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
-            "s_nop 1"
-            : "=&v"(r[0])
-            : "v"(x[0]), "v"(x[1]));
-        }
-        else if constexpr (NP == 2) {
-            asm("s_nop 1\n\t"
-            "v_add_f32_dpp %0, %2, %2 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
-            "v_add_f32_dpp %0, %3, %3 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
-            "v_add_f32_dpp %1, %4, %4 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
-            "v_add_f32_dpp %1, %5, %5 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
-            "s_nop 1"
-            : "=&v"(r[0]), "=&v"(r[1])
-            : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]));
-        }
-        else if constexpr (NP == 4) {
-            asm("s_nop 1\n\t"
-            "v_add_f32_dpp %0, %4, %4 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
-            "v_add_f32_dpp %0, %5, %5 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
-            "v_add_f32_dpp %1, %6, %6 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
-            "v_add_f32_dpp %1, %7, %7 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
-            "v_add_f32_dpp %2, %8, %8 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
-            "v_add_f32_dpp %2, %9, %9 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
-            "v_add_f32_dpp %3, %10, %10 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
-            "v_add_f32_dpp %3, %11, %11 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
-            "s_nop 1"
-            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
-            : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]), "v"(x[5]), "v"(x[6]), "v"(x[7]));
-        }
-        else if constexpr (NP == 8) {
-            asm("s_nop 1\n\t"
-            "v_add_f32_dpp %0, %8, %8 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
-            "v_add_f32_dpp %0, %9, %9 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
-            "v_add_f32_dpp %1, %10, %10 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
-            "v_add_f32_dpp %1, %11, %11 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
-            "v_add_f32_dpp %2, %12, %12 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
-            "v_add_f32_dpp %2, %13, %13 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
-            "v_add_f32_dpp %3, %14, %14 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
-            "v_add_f32_dpp %3, %15, %15 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
-            "v_add_f32_dpp %4, %16, %16 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
-            "v_add_f32_dpp %4, %17, %17 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
-            "v_add_f32_dpp %5, %18, %18 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
-            "v_add_f32_dpp %5, %19, %19 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
-            "v_add_f32_dpp %6, %20, %20 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
-            "v_add_f32_dpp %6, %21, %21 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
-            "v_add_f32_dpp %7, %22, %22 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
-            "v_add_f32_dpp %7, %23, %23 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
-            "s_nop 1"
-            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
-            : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]), "v"(x[5]), "v"(x[6]), "v"(x[7]), "v"(x[8]), "v"(x[9]), "v"(x[10]), "v"(x[11]), "v"(x[12]), "v"(x[13]), "v"(x[14]), "v"(x[15]));
-        }
-    }
-}
+MWC_BANK_LEVEL(3, "row_mirror", "0x3", "0xc")       // lane bit i3: banks 0,1 keep half 0
+MWC_BANK_LEVEL(2, "row_half_mirror", "0x5", "0xa")  // lane bit i2: banks 0,2 keep half 0
+#undef MWC_BANK_LEVEL
+#undef MWC_BANK_ADD
+
 template <int G, int V, int L = 0, int M = V>
 __device__ __forceinline__ float reduce_scatter_lv(float (&x)[V], int lane) {
     static_assert(V >= 2 && V <= G && (V & (V - 1)) == 0 && (G & (G - 1)) == 0 && G <= 16, "shape");
