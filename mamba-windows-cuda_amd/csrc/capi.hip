@@ -146,9 +146,9 @@ SegPlan plan(const SsmShape& s, bool bwd, int spl, int cap_main, int cap_carry, 
 // Workgroups per CU each kernel fits, by SPL: min(512 / VGPRs per lane, 160 KB / LDS per
 // workgroup), from the gfx950 build's resource usage.
 int fwd_cap(int spl) { return spl == 1 ? 5 : spl == 2 ? 3 : 1; }
-int fwd_carry_cap(int spl) { return spl == 1 ? 6 : spl == 2 ? 4 : 2; }
+int fwd_carry_cap(int spl) { return spl == 1 ? 8 : spl == 2 ? 6 : 4; }
 int bwd_cap(int spl) { return spl == 4 ? 1 : 3; }
-int bwd_carry_cap(int spl) { return spl == 1 ? 5 : spl == 2 ? 4 : 2; }
+int bwd_carry_cap(int spl) { return spl == 1 ? 8 : spl == 2 ? 6 : 4; }
 
 size_t carry_bytes(const SsmShape& s, const SegPlan& p) {
     return p.nseg > 1 ? align256((size_t)s.batch * p.ncar * s.dim * s.nstate * sizeof(float)) : 0;

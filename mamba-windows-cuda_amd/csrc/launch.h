@@ -18,6 +18,10 @@ bool lane_group_supported(int ns, int spl);
 // Waves per SIMD the lane-group kernels are compiled to fit (each lane then has 512/W VGPRs).
 constexpr int fwd_min_waves(int spl) { return spl == 4 ? 1 : 3; }
 constexpr int bwd_min_waves(int spl) { return spl == 4 ? 1 : 3; }
+#ifndef MWC_CARRY_WAVES
+#define MWC_CARRY_WAVES 6
+#endif
+constexpr int carry_min_waves(int spl) { return spl == 4 ? 1 : MWC_CARRY_WAVES; }
 
 // Launch plan of the lane-group kernels: SPL = states held per lane (16/SPL lanes per channel),
 // nseg = segments L is cut into (cps chunks of kCkptSteps steps each), cfold = carry segments per

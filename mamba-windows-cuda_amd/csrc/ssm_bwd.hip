@@ -95,7 +95,7 @@ __device__ __forceinline__ void wave_lds_fence() {
 // segment from g = 0, car_x = its summed base-2 decay exponents (so it maps an
 // adjoint g arriving from its right to 2^car_x * g + car_g).
 template <typename T, int NS, int SPL, bool XF>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fwd_min_waves(SPL), 8)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(carry_min_waves(SPL), 8)))
 ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const T* __restrict__ Cm,
                      const T* __restrict__ dout, float* __restrict__ car_g, float* __restrict__ car_x, int Bsz,
                      int L, int D, int nck, int nblk_d, int ncar, int first, int cps, ScanXf xf) {
@@ -215,17 +215,28 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
         const int buf = k & 1;
         const bool more = k > k0;
         if (more) issue(k - 1);
+        // operands are read four steps at a time, which keeps the pass to few enough registers for
+        // twice the waves per SIMD (its chunks are short on arithmetic, so more waves in flight are
+        // what covers the loads)
         float dt[TC], yo[TC], Cv[TC][SPL];
-        ldv<TC>(&s_in[buf][0][c][0], dt);
-        ldv<TC>(&s_in[buf][1][c][0], yo);
+        auto read_steps = [&](int i0) {
+            float t4[4], y4[4];
+            ldv<4>(&s_in[buf][0][c][i0], t4);
+            ldv<4>(&s_in[buf][1][c][i0], y4);
 #pragma unroll
-        for (int i = 0; i < TC; ++i) ldv<SPL>(&s_c[buf][i][n0], Cv[i]);
+            for (int q = 0; q < 4; ++q) {
+                dt[i0 + q] = t4[q];
+                yo[i0 + q] = y4[q];
+                ldv<SPL>(&s_c[buf][i0 + q][n0], Cv[i0 + q]);
+            }
+        };
         // one workgroup-uniform decision per chunk (exact: see the main kernel)
         const bool need_clamp = __builtin_amdgcn_readfirstlane(s_flag[buf]) == k;
         auto run = [&](auto clamp_tag) {
             constexpr bool CLAMP = decltype(clamp_tag)::value;
 #pragma unroll
             for (int i = TC - 1; i >= 0; --i) {
+                if (i % 4 == 3) read_steps(i - 3);
 #pragma unroll
                 for (int j = 0; j < SPL; ++j) {
                     float x = dt[i] * A2[j];

@@ -76,7 +76,7 @@ enum FwdMode { kMain = 0, kState = 1, kCarry = 2 };
 // XF: the elementwise transforms of ScanXf are compiled in (the plain scan does not carry their
 // registers).
 template <typename T, int NS, int SPL, int MODE, bool XF>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fwd_min_waves(SPL), 8)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == 2 ? carry_min_waves(SPL) : fwd_min_waves(SPL), 8)))
 ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __restrict__ A,
                const T* __restrict__ Bm, const T* __restrict__ Cm, const T* __restrict__ Dv,
                const T* __restrict__ h_prev, T* __restrict__ out, T* __restrict__ h_last, float* __restrict__ ckpt,
@@ -256,24 +256,39 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
         if (more) issue(k + 1);
         if (ckb != nullptr && valid) vst<SPL>(ckb + (int64_t)k * D * NS, h);
 
-        // the whole chunk's operands, read up front so LDS latency is paid once per chunk
+        // the main pass reads the whole chunk's operands up front, so LDS latency is paid once per
+        // chunk; the state-only passes read them four steps at a time, which keeps them to few enough
+        // registers for twice the waves per SIMD (their chunks are short on arithmetic, so more waves
+        // in flight are what covers the loads)
         float dt[TC], dtu[TC], Bv[TC][SPL], Cv[TC][SPL];
-        lds_ld<TC>(&s_in[buf][0][c][0], dt);
-        lds_ld<TC>(&s_in[buf][1][c][0], dtu);
+        auto read_steps = [&](int i0, int n) {
 #pragma unroll
-        for (int i = 0; i < TC; ++i) {
-            if constexpr (HAS_OUT) {
-                float bc[2 * SPL];
-                lds_ld<2 * SPL>(&s_bc[buf][i][2 * n0], bc);
+            for (int i4 = i0; i4 < i0 + n; i4 += 4) {
+                float t4[4], u4[4];
+                lds_ld<4>(&s_in[buf][0][c][i4], t4);
+                lds_ld<4>(&s_in[buf][1][c][i4], u4);
 #pragma unroll
-                for (int j = 0; j < SPL; ++j) {
-                    Bv[i][j] = bc[j];
-                    Cv[i][j] = bc[SPL + j];
+                for (int q = 0; q < 4; ++q) {
+                    dt[i4 + q] = t4[q];
+                    dtu[i4 + q] = u4[q];
                 }
-            } else {
-                lds_ld<SPL>(&s_bc[buf][i][n0], Bv[i]);
             }
-        }
+#pragma unroll
+            for (int i = i0; i < i0 + n; ++i) {
+                if constexpr (HAS_OUT) {
+                    float bc[2 * SPL];
+                    lds_ld<2 * SPL>(&s_bc[buf][i][2 * n0], bc);
+#pragma unroll
+                    for (int j = 0; j < SPL; ++j) {
+                        Bv[i][j] = bc[j];
+                        Cv[i][j] = bc[SPL + j];
+                    }
+                } else {
+                    lds_ld<SPL>(&s_bc[buf][i][n0], Bv[i]);
+                }
+            }
+        };
+        if constexpr (HAS_OUT) read_steps(0, TC);
         // one workgroup-uniform decision per chunk: the loaders flag a chunk in which some |delta*A|
         // can exceed 88; the clamped path gives the same values whenever none does, so deciding for the
         // whole workgroup is exact
@@ -287,6 +302,9 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
             constexpr bool CLAMP = decltype(clamp_tag)::value;
 #pragma unroll
             for (int i = 0; i < TC; ++i) {
+                if constexpr (!HAS_OUT) {
+                    if (i % 4 == 0) read_steps(i, 4);
+                }
                 float y = 0.f;
 #pragma unroll
                 for (int j = 0; j < SPL; ++j) {
