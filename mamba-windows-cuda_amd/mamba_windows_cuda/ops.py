@@ -30,8 +30,35 @@ def _ptr(t):
     return None if t is None else t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(dev: torch.device):
+    """The current HIP stream of `dev` (a raw hipStream_t as an int)."""
+    if _raw_stream is not None:
+        return _raw_stream(dev.index)
     return torch.cuda.current_stream(dev).cuda_stream
+
+
+class _on_device:
+    """Makes `dev` the current HIP device for a launch; costs nothing when it already is (the usual
+    case), unlike ``torch.cuda.device``, which switches and restores every time."""
+
+    __slots__ = ("idx", "prev")
+
+    def __init__(self, dev: torch.device):
+        self.idx = dev.index
+
+    def __enter__(self):
+        self.prev = torch.cuda.current_device()
+        if self.prev != self.idx:
+            torch.cuda.set_device(self.idx)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev != self.idx:
+            torch.cuda.set_device(self.prev)
+        return False
 
 
 def _require(cond: bool, msg: str) -> None:
@@ -119,7 +146,7 @@ def ssm_forward_xf(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, *, delta_bias=
             if want_ckpt else None)
     nbytes = L_.mwc_ssm_fwd_workspace_size(bsz, L, dm, n)
     ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
-    with torch.cuda.device(dev):
+    with _on_device(dev):
         st = L_.mwc_ssm_fwd_ex(_dtype_code(u), _ptr(u), _ptr(delta), _ptr(A), _ptr(B_ssm), _ptr(C_ssm),
                                _ptr(D_ssm), _ptr(h_prev), _ptr(delta_bias), int(bool(delta_softplus)), _ptr(z),
                                _ptr(out), _ptr(out_z), _ptr(h_last), _ptr(ckpt), bsz, L, dm, n,
@@ -172,7 +199,7 @@ def ssm_backward_xf(u, delta, A, B_ssm, C_ssm, D_ssm, dout, ckpt, dh_last=None, 
     dz = torch.empty_like(z) if z is not None else None
     nbytes = L_.mwc_ssm_bwd_workspace_size(bsz, L, dm, n)
     ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
-    with torch.cuda.device(dev):
+    with _on_device(dev):
         st = L_.mwc_ssm_bwd_ex(_dtype_code(u), _ptr(u), _ptr(delta), _ptr(A), _ptr(B_ssm), _ptr(C_ssm),
                                _ptr(D_ssm), None, _ptr(delta_bias), int(bool(delta_softplus)), _ptr(z),
                                _ptr(out_ungated if z is not None else None), _ptr(dout), _ptr(dh_last), _ptr(ckpt),
@@ -224,7 +251,7 @@ def ssm_step(u, delta, A, B_ssm, C_ssm, D_ssm, h, *, delta_bias=None, delta_soft
              "out_state must be a contiguous, 4-element-aligned (B, D, N) tensor of u's dtype")
     out = torch.empty_like(u)
     L_ = _lib.lib()
-    with torch.cuda.device(u.device):
+    with _on_device(u.device):
         st = L_.mwc_ssm_step(_dtype_code(u), _ptr(u), _ptr(delta), _ptr(A), _ptr(B_ssm), _ptr(C_ssm), _ptr(D_ssm),
                              _ptr(h), _ptr(delta_bias), int(bool(delta_softplus)), _ptr(z),
                              None if z is not None else _ptr(out), _ptr(out) if z is not None else None,
@@ -262,7 +289,7 @@ def pscan_forward(A, X):
     L_ = _lib.lib()
     nbytes = L_.mwc_pscan_workspace_size(nseq, L, nc)
     ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=X.device)
-    with torch.cuda.device(X.device):
+    with _on_device(X.device):
         st = L_.mwc_pscan_fwd(_dtype_code(X), a3.data_ptr(), x3.data_ptr(), h3.data_ptr(), nseq, L, nc,
                               ws.data_ptr(), nbytes, _stream(X.device))
     _lib.check(st, "mwc_pscan_fwd")
@@ -279,7 +306,7 @@ def pscan_backward(A, H, dH):
     L_ = _lib.lib()
     nbytes = L_.mwc_pscan_workspace_size(nseq, L, nc)
     ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=H.device)
-    with torch.cuda.device(H.device):
+    with _on_device(H.device):
         st = L_.mwc_pscan_bwd(_dtype_code(H), a3.data_ptr(), h3.data_ptr(), g3.data_ptr(), da3.data_ptr(),
                               dx3.data_ptr(), nseq, L, nc, ws.data_ptr(), nbytes, _stream(H.device))
     _lib.check(st, "mwc_pscan_bwd")
