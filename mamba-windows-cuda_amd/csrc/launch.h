@@ -16,7 +16,7 @@ struct SsmShape {
 bool lane_group_supported(int ns, int spl);
 
 // Waves per SIMD the lane-group kernels are compiled to fit (each lane then has 512/W VGPRs).
-constexpr int fwd_min_waves(int spl) { return spl == 4 ? 1 : 3; }
+constexpr int fwd_min_waves(int spl) { return spl == 4 ? 1 : spl == 1 ? 6 : 3; }
 constexpr int bwd_min_waves(int spl) { return spl == 4 ? 1 : 3; }
 #ifndef MWC_CARRY_WAVES
 #define MWC_CARRY_WAVES 6

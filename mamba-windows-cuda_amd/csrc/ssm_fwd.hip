@@ -288,7 +288,9 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
                 }
             }
         };
-        if constexpr (HAS_OUT) read_steps(0, TC);
+        // the main pass at one state per lane runs many waves per SIMD too, and reads in groups as well
+        constexpr bool GROUPED = !HAS_OUT || SPL == 1;
+        if constexpr (!GROUPED) read_steps(0, TC);
         // one workgroup-uniform decision per chunk: the loaders flag a chunk in which some |delta*A|
         // can exceed 88; the clamped path gives the same values whenever none does, so deciding for the
         // whole workgroup is exact
@@ -302,7 +304,7 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
             constexpr bool CLAMP = decltype(clamp_tag)::value;
 #pragma unroll
             for (int i = 0; i < TC; ++i) {
-                if constexpr (!HAS_OUT) {
+                if constexpr (GROUPED) {
                     if (i % 4 == 0) read_steps(i, 4);
                 }
                 float y = 0.f;
