@@ -145,7 +145,7 @@ int mwc_ssm_bwd_ex(int dtype, const void* u, const void* delta, const void* A, c
  * batched layout without the length axis:
  *   u, delta, z, out, out_z (batch, dim); B_ssm, C_ssm (batch, N); h, h_new (batch, dim, N).
  * h_new may alias h (in-place update). out may be NULL; out_z must be given with z (and only then).
- * A, B_ssm, C_ssm, h and h_new must be aligned to 4 elements.
+ * A, B_ssm, C_ssm, h and h_new must be aligned to 16 bytes.
  * Replaces selective_scan_cuda_forward_with_state (mamba_cuda.py:271-359) called with seqlen 1,
  * the reference's only way to advance one step; needs no workspace.
  */

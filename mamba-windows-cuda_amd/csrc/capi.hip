@@ -329,10 +329,10 @@ int mwc_ssm_step(int dtype, const void* u, const void* delta, const void* A, con
         return fail(MWC_ERR_INVALID_ARGUMENT, "u, delta, A, B_ssm, C_ssm, D_ssm, h and h_new must not be NULL");
     if (z != nullptr && out_z == nullptr) return fail(MWC_ERR_INVALID_ARGUMENT, "out_z must not be NULL when z is given");
     if (z == nullptr && out_z != nullptr) return fail(MWC_ERR_INVALID_ARGUMENT, "out_z needs z");
-    const uintptr_t align = 4 * (dtype == MWC_DTYPE_F16 ? 2 : 4);  // 4 states per vector access
+    const uintptr_t align = 16;  // the kernel moves a lane's states as one 16-byte vector
     for (const void* p : {A, B_ssm, C_ssm, h, static_cast<const void*>(h_new)})
         if ((uintptr_t)p % align != 0)
-            return fail(MWC_ERR_INVALID_ARGUMENT, "A, B_ssm, C_ssm, h and h_new must be aligned to 4 elements");
+            return fail(MWC_ERR_INVALID_ARGUMENT, "A, B_ssm, C_ssm, h and h_new must be aligned to 16 bytes");
     MWC_HIP_TRY(mwc::launch_ssm_step(dtype, (int)dstate, u, delta, A, B_ssm, C_ssm, D_ssm, h,
                                      mwc::ScanXf{delta_bias, z, delta_softplus != 0}, out, out_z, h_new, batch, dim,
                                      (hipStream_t)stream));

@@ -6,16 +6,19 @@
 // y_z = y * silu(z)). The state is read and written in the input dtype, (batch, dim, N), and the
 // output state may alias the input one (in-place update).
 //
-// Mapping: N/4 consecutive lanes hold one channel's N states, 4 per lane, so the state moves as
-// coalesced rows of 8- or 16-byte accesses and the C-contraction is an in-lane FMA chain plus a
-// DPP sum over the N/4 lanes. The step is bound by the state's round trip through HBM
-// (2 * batch * dim * N * s bytes) and, at small batch, by launch latency.
+// Mapping: a lane holds 16 bytes of a channel's states (4 fp32 or 8 fp16/bf16 states), so the state,
+// A, B and C move as coalesced rows of 16-byte accesses, and the C-contraction is an in-lane FMA
+// chain plus a DPP sum over the channel's N*s/16 lanes. The step is bound by the state's round trip
+// through HBM (2 * batch * dim * N * s bytes) and, at small batch, by launch latency.
 #include "common.h"
 #include "launch.h"
 
 namespace mwc {
 
-constexpr int kStepSpl = 4;  // states per lane (NS / 4 lanes per channel)
+// states per lane: one 16-byte vector of the storage type (all N states when they are fewer)
+template <typename T, int NS> constexpr int step_spl() {
+    return (int)(16 / sizeof(T)) < NS ? (int)(16 / sizeof(T)) : NS;
+}
 
 template <typename T, int NS>
 __global__ void __launch_bounds__(256) ssm_step_kernel(const T* __restrict__ u, const T* __restrict__ delta,
@@ -23,6 +26,7 @@ __global__ void __launch_bounds__(256) ssm_step_kernel(const T* __restrict__ u, 
                                                        const T* __restrict__ Cm, const T* __restrict__ Dv,
                                                        const T* h_in, ScanXf xf, T* __restrict__ y,
                                                        T* __restrict__ y_z, T* h_out, int64_t channels, int D) {
+    constexpr int kStepSpl = step_spl<T, NS>();
     constexpr int kStepLpc = NS / kStepSpl;
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // over batch * dim * kStepLpc
     const int n0 = (int)(i % kStepLpc) * kStepSpl;
@@ -36,8 +40,8 @@ __global__ void __launch_bounds__(256) ssm_step_kernel(const T* __restrict__ u, 
     if (xf.softplus) dt = softplus_f(dt);
     const float uu = ld(u + bdc);
     const float dtu = dt * uu;
-    // 4 consecutive states per lane: one 8-byte (fp16) or 16-byte (fp32) access per tensor
-    typedef T vec4 __attribute__((ext_vector_type(4)));
+    // kStepSpl consecutive states per lane: one 16-byte access per tensor
+    typedef T vec4 __attribute__((ext_vector_type(kStepSpl)));
     const vec4 a4 = *reinterpret_cast<const vec4*>(A + (int64_t)d * NS + n0);
     const vec4 h4 = *reinterpret_cast<const vec4*>(h_in + bdc * NS + n0);
     const vec4 b4 = *reinterpret_cast<const vec4*>(Bm + b * NS + n0);
@@ -68,11 +72,11 @@ hipError_t launch_ssm_step(int dt, int ns, const void* u, const void* delta, con
                            const void* C, const void* Dv, const void* h_in, const ScanXf& xf, void* y, void* y_z,
                            void* h_out, int64_t batch, int64_t dim, hipStream_t st) {
     const int64_t channels = batch * dim;
-    const int64_t lanes = channels * (ns / kStepSpl);
-    const int grid = (int)((lanes + 255) / 256);
 #define MWC_STEP(N)                                                                                            \
     if (ns == N) {                                                                                             \
         MWC_DISPATCH_DTYPE(dt, TT,                                                                             \
+                           const int64_t lanes = channels * (N / step_spl<TT, N>());                          \
+                           const int grid = (int)((lanes + 255) / 256);                                        \
                            hipLaunchKernelGGL((ssm_step_kernel<TT, N>), dim3(grid), dim3(256), 0, st,          \
                                               (const TT*)u, (const TT*)delta, (const TT*)A, (const TT*)B,      \
                                               (const TT*)C, (const TT*)Dv, (const TT*)h_in, xf, (TT*)y,        \

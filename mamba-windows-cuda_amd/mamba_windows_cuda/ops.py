@@ -234,7 +234,7 @@ def ssm_step(u, delta, A, B_ssm, C_ssm, D_ssm, h, *, delta_bias=None, delta_soft
         if t is not None:
             _require(tuple(t.shape) == shape, f"{name} shape must be {shape}")
             _require(t.dtype == u.dtype and t.device == u.device, f"{name} must match u's dtype and device")
-    align = 4 * u.element_size()  # the kernel moves 4 states per vector access
+    align = 16  # the kernel moves a lane's states as one 16-byte vector
 
     def aligned(t):
         t = t.contiguous()
@@ -248,7 +248,7 @@ def ssm_step(u, delta, A, B_ssm, C_ssm, D_ssm, h, *, delta_bias=None, delta_soft
         out_state = torch.empty_like(h)
     _require(out_state.is_contiguous() and tuple(out_state.shape) == (bsz, dm, n) and out_state.dtype == u.dtype
              and out_state.data_ptr() % align == 0,
-             "out_state must be a contiguous, 4-element-aligned (B, D, N) tensor of u's dtype")
+             "out_state must be a contiguous, 16-byte-aligned (B, D, N) tensor of u's dtype")
     out = torch.empty_like(u)
     L_ = _lib.lib()
     with _on_device(u.device):
