@@ -108,3 +108,26 @@ def test_step_graph_replay(dev):
         torch.cuda.synchronize()
     assert torch.equal(h, h_eager)
     assert torch.equal(y2, y_eager)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_step_misaligned_state(dev, dtype):
+    """The step moves a lane's states as one 16-byte vector: a state view that starts off a 16-byte
+    boundary is copied by the Python layer (same result as an aligned one), and an out_state view that
+    does is refused with RuntimeError."""
+    Bsz, D = 3, 130
+    x = _step_inputs(Bsz, D, dtype, seed=5)
+    xd = {k: v.to(dev) for k, v in x.items()}
+    m = SelectiveScanCuda()
+    args = (xd["u"][:, 0], xd["delta"][:, 0], xd["A"], xd["B"][:, 0], xd["C"][:, 0], xd["D"])
+    # the same state, starting one element (4 or 2 bytes) past a 16-byte boundary
+    buf = torch.zeros(Bsz * D * 16 + 1, dtype=dtype, device=dev)
+    h_off = buf[1:].view(Bsz, D, 16)
+    h_off.copy_(xd["h_prev"])
+    assert h_off.data_ptr() % 16 != 0
+    with torch.no_grad():
+        y_ref, h_ref = m.step(*args, xd["h_prev"])
+        y, h = m.step(*args, h_off)
+        assert torch.equal(y, y_ref) and torch.equal(h, h_ref)
+        with pytest.raises(RuntimeError, match="16-byte-aligned"):
+            m.step(*args, xd["h_prev"], out_state=h_off)
