@@ -84,14 +84,30 @@ template <> __device__ __forceinline__ void buf_st<bf16_t>(rsrc_t r, uint32_t of
 // t - t^2/2 + t^3/3 for t = e^x < 2^-6 (where 1 + t would round away t's low bits; the first
 // omitted term is below 2^-20 relative), else ln2 * log2(1 + t).
 constexpr float kLn2 = 0.6931471805599453f;
+// Both forms are computed and then selected, so the code is straight-line rather than a divergent
+// branch; the unselected form may be inf or NaN above the threshold, and a NaN x stays NaN.
 __device__ __forceinline__ float softplus_f(float x) {
     const float t = __builtin_amdgcn_exp2f(x * kLog2e);
-    const float series = t * __builtin_fmaf(t, __builtin_fmaf(t, 1.f / 3.f, -0.5f), 1.f);
-    const float big = kLn2 * __builtin_amdgcn_logf(1.f + t);
+    float series = t * __builtin_fmaf(t, __builtin_fmaf(t, 1.f / 3.f, -0.5f), 1.f);
+    float big = kLn2 * __builtin_amdgcn_logf(1.f + t);
+    asm("" : "+v"(series), "+v"(big));
     return x > 20.f ? x : (t < 0.015625f ? series : big);
 }
 __device__ __forceinline__ float sigmoid_f(float x) {
     return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * kLog2e));
+}
+// softplus(x) and its derivative sigmoid(x) = t / (1 + t), sharing the one exponential t = e^x;
+// above the threshold sigmoid(x) is 1 in fp32
+__device__ __forceinline__ float softplus_grad_f(float x, float& sig) {
+    const float t = __builtin_amdgcn_exp2f(x * kLog2e);
+    const float u = 1.f + t;
+    float s = t * __builtin_amdgcn_rcpf(u);
+    float series = t * __builtin_fmaf(t, __builtin_fmaf(t, 1.f / 3.f, -0.5f), 1.f);
+    float big = kLn2 * __builtin_amdgcn_logf(u);
+    asm("" : "+v"(series), "+v"(big), "+v"(s));
+    const bool above = x > 20.f;
+    sig = above ? 1.f : s;
+    return above ? x : (t < 0.015625f ? series : big);
 }
 
 // DPP lane exchanges within 16-lane rows (gfx9 DPP controls).

@@ -45,6 +45,11 @@ struct ScanXf {
     const void* z;           // (batch, seqlen, dim)
     int softplus;
 };
+// The scan kernels are compiled per set of transforms (a template bit mask), so the plain scan
+// carries none of their registers and no kernel tests for a transform it does not apply inside its
+// chunk loop: kXfDelta = delta' = softplus?(delta + delta_bias?) (bias and softplus stay run-time
+// flags), kXfGate = the z gate.
+constexpr int kXfDelta = 1, kXfGate = 2;
 
 struct FwdArgs {
     const void *u, *delta, *A, *B, *C, *Dv, *h_prev;

@@ -94,7 +94,7 @@ __device__ __forceinline__ void wave_lds_fence() {
 // car_g = the reverse sweep of g -> dA_t * (g + dout_t * C_t) over the carry
 // segment from g = 0, car_x = its summed base-2 decay exponents (so it maps an
 // adjoint g arriving from its right to 2^car_x * g + car_g).
-template <typename T, int NS, int SPL, bool XF>
+template <typename T, int NS, int SPL, int XF>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(carry_min_waves(SPL), 8)))
 ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const T* __restrict__ Cm,
                      const T* __restrict__ dout, float* __restrict__ car_g, float* __restrict__ car_x, int Bsz,
@@ -150,9 +150,9 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
     // buffer resources per chunk: rows past L and channels past D read as 0 (see the main kernel)
     const uint32_t lofs = lvalid ? ((uint32_t)(sg * SPG) * (uint32_t)D + (uint32_t)ld_d) * sizeof(T) : kOob;
     const uint32_t row_bytes = (uint32_t)D * sizeof(T);
-    const T* zb = XF && xf.z ? static_cast<const T*>(xf.z) : nullptr;
-    const bool xform = XF && (xf.delta_bias != nullptr || xf.softplus);
-    const float lbias = XF && xf.delta_bias ? ld(static_cast<const T*>(xf.delta_bias) + ld_d) : 0.f;
+    constexpr bool XD = (XF & kXfDelta) != 0, XG = (XF & kXfGate) != 0;
+    const T* zb = XG ? static_cast<const T*>(xf.z) : nullptr;
+    const float lbias = XD && xf.delta_bias ? ld(static_cast<const T*>(xf.delta_bias) + ld_d) : 0.f;
     T pd[SPG], py[SPG], pz[SPG], pc[BCPT];
     auto issue = [&](int k) {
         const int64_t ck = (int64_t)k * TC;
@@ -164,7 +164,7 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
             pd[s] = buf_raw<T>(rd, lofs + s * row_bytes);
             py[s] = buf_raw<T>(ry, lofs + s * row_bytes);
         }
-        if (XF && zb != nullptr) {
+        if constexpr (XG) {
             const rsrc_t rz = make_rsrc(zb + (row0 + ck) * D, rows * row_bytes);
 #pragma unroll
             for (int s = 0; s < SPG; ++s) pz[s] = buf_raw<T>(rz, lofs + s * row_bytes);
@@ -180,17 +180,26 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
         for (int s = 0; s < SPG; ++s) {
             vd[s] = static_cast<float>(pd[s]);
             vy[s] = static_cast<float>(py[s]);
-            if constexpr (XF) {
-                if (xform) {
-                    vd[s] += lbias;
-                    if (xf.softplus) vd[s] = softplus_f(vd[s]);
-                    if (k * TC + sg * SPG + s >= L) vd[s] = 0.f;
-                }
-                if (zb != nullptr) {  // the scan sees dout * silu(z)
-                    const float zv = static_cast<float>(pz[s]);
-                    vy[s] *= zv * sigmoid_f(zv);
-                }
+            if constexpr (XG) {  // the scan sees dout * silu(z)
+                const float zv = static_cast<float>(pz[s]);
+                vy[s] *= zv * sigmoid_f(zv);
             }
+        }
+        if constexpr (XD) {
+#pragma unroll
+            for (int s = 0; s < SPG; ++s) vd[s] += lbias;  // 0 without a bias
+            if (xf.softplus) {
+#pragma unroll
+                for (int s = 0; s < SPG; ++s) vd[s] = softplus_f(vd[s]);
+            }
+            if ((k + 1) * TC > L) {  // the ragged last chunk: padded steps keep delta' = 0
+#pragma unroll
+                for (int s = 0; s < SPG; ++s)
+                    if (k * TC + sg * SPG + s >= L) vd[s] = 0.f;
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < SPG; ++s) {
             vmax = __builtin_fmaxf(vmax, __builtin_fabsf(vd[s]));
             sdt_l += vd[s];
         }
@@ -272,9 +281,8 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
     }
 }
 
-// XF: the elementwise transforms of ScanXf are compiled in (the plain scan does not carry their
-// registers).
-template <typename T, int NS, int SPL, bool XF>
+// XF: the transforms of ScanXf compiled in (kXfDelta, kXfGate bits).
+template <typename T, int NS, int SPL, int XF>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_min_waves(SPL), 8)))
 ssm_bwd_kernel(
     const T* __restrict__ u, const T* __restrict__ delta, const T* __restrict__ A, const T* __restrict__ Bm,
@@ -369,8 +377,8 @@ ssm_bwd_kernel(
     const uint32_t row_bytes = (uint32_t)D * sizeof(T);
     auto chunk_rows = [&](int k) { return (uint32_t)min(TC, L - k * TC); };
     const int64_t rowD = row0 * D;
-    const T* zb = XF && xf.z ? static_cast<const T*>(xf.z) : nullptr;
-    const bool xform = XF && (xf.delta_bias != nullptr || xf.softplus);
+    constexpr bool XD = (XF & kXfDelta) != 0, XG = (XF & kXfGate) != 0;
+    const T* zb = XG ? static_cast<const T*>(xf.z) : nullptr;
     T pu[SPG], pd[SPG], py[SPG], pz[SPG], pyo[SPG], pb[BCPT], pc[BCPT];
     float hnext[SPL];
     auto issue = [&](int k) {
@@ -385,7 +393,7 @@ ssm_bwd_kernel(
             pd[s] = buf_raw<T>(rd, lofs + s * row_bytes);
             py[s] = buf_raw<T>(ry, lofs + s * row_bytes);
         }
-        if (XF && zb != nullptr) {  // z and the ungated output, for dout * silu(z) and dz
+        if constexpr (XG) {  // z and the ungated output, for dout * silu(z) and dz
             const rsrc_t rz = make_rsrc(zb + rowD + ck * D, rows * row_bytes);
             const rsrc_t ro = make_rsrc(yb_out + rowD + ck * D, rows * row_bytes);
 #pragma unroll
@@ -408,9 +416,9 @@ ssm_bwd_kernel(
 #pragma unroll
     for (int n = 0; n < NS; ++n) lamax2 = __builtin_fmaxf(lamax2, __builtin_fabsf(ld(A + (int64_t)ld_d * NS + n)));
     lamax2 *= kLog2e;
-    const float lbias = XF && xf.delta_bias ? ld(static_cast<const T*>(xf.delta_bias) + ld_d) : 0.f;
-    // d delta / d delta' (softplus) of the loader's elements, for the chunk being stored and the next
-    float dd_cur[XF ? SPG : 1], dd_nxt[XF ? SPG : 1];
+    const float lbias = XD && xf.delta_bias ? ld(static_cast<const T*>(xf.delta_bias) + ld_d) : 0.f;
+    // d delta' / d delta (softplus) of the loader's elements, for the chunk being stored and the next
+    float dd_cur[XD ? SPG : 1], dd_nxt[XD ? SPG : 1];
     float dbias_acc = 0.f;
     // the loader's (channel, steps) elements of the chunk being stored and of the next one: delta and
     // dout (as the scan sees them), for du = D*dout + delta*sum_n g*B; dD accumulates here, once per
@@ -427,35 +435,43 @@ ssm_bwd_kernel(
             vd[s] = static_cast<float>(pd[s]);
             vu[s] = static_cast<float>(pu[s]);
             vy[s] = static_cast<float>(py[s]);
-            if constexpr (XF) {
-                dd_nxt[s] = 1.f;
-                if (xform) {
-                    vd[s] += lbias;
-                    if (xf.softplus) {
-                        dd_nxt[s] = sigmoid_f(vd[s]);
-                        vd[s] = softplus_f(vd[s]);
-                    }
-                    if (k * TC + sg * SPG + s >= L) vd[s] = 0.f;
-                }
-                if (zb != nullptr) {  // out_z = out * silu(z): the scan sees dout * silu(z)
-                    const float zv = static_cast<float>(pz[s]);
-                    const float sz = sigmoid_f(zv);
-                    vdz[s] = vy[s] * static_cast<float>(pyo[s]) * sz * (1.f + zv * (1.f - sz));
-                    vy[s] *= zv * sz;
-                }
+            if constexpr (XG) {  // out_z = out * silu(z): the scan sees dout * silu(z)
+                const float zv = static_cast<float>(pz[s]);
+                const float sz = sigmoid_f(zv);
+                const float a = vy[s] * sz;
+                // silu'(z) = sigmoid(z) * (1 + z * (1 - sigmoid(z)))
+                vdz[s] = a * static_cast<float>(pyo[s]) * __builtin_fmaf(zv, 1.f - sz, 1.f);
+                vy[s] = a * zv;
             }
+        }
+        if constexpr (XD) {
+#pragma unroll
+            for (int s = 0; s < SPG; ++s) {
+                vd[s] += lbias;  // 0 without a bias
+                dd_nxt[s] = 1.f;
+            }
+            if (xf.softplus) {
+#pragma unroll
+                for (int s = 0; s < SPG; ++s) vd[s] = softplus_grad_f(vd[s], dd_nxt[s]);
+            }
+            if ((k + 1) * TC > L) {  // the ragged last chunk: padded steps keep delta' = 0
+#pragma unroll
+                for (int s = 0; s < SPG; ++s)
+                    if (k * TC + sg * SPG + s >= L) vd[s] = 0.f;
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < SPG; ++s) {
             vdu[s] = vd[s] * vu[s];
             vmax = __builtin_fmaxf(vmax, __builtin_fabsf(vd[s]));
             d_nxt[s] = vd[s];
             y_nxt[s] = vy[s];
             dDl = __builtin_fmaf(vy[s], vu[s], dDl);  // rows past L read as 0
         }
-        if constexpr (XF) {
-            if (zb != nullptr) {  // dz = dout * out * silu'(z) needs no scan: store it now
-                const rsrc_t rdz = make_rsrc(dz + rowD + (int64_t)k * TC * D, chunk_rows(k) * row_bytes);
+        if constexpr (XG) {  // dz = dout * out * silu'(z) needs no scan: store it now
+            const rsrc_t rdz = make_rsrc(dz + rowD + (int64_t)k * TC * D, chunk_rows(k) * row_bytes);
 #pragma unroll
-                for (int s = 0; s < SPG; ++s) buf_st<T>(rdz, lofs + s * row_bytes, vdz[s]);
-            }
+            for (int s = 0; s < SPG; ++s) buf_st<T>(rdz, lofs + s * row_bytes, vdz[s]);
         }
         if (vmax * lamax2 > kExp2Clamp) s_flag = k;  // benign race: every writer stores k
         stv<SPG>((s_in(0, lc) + sg * SPG), vd);
@@ -495,7 +511,7 @@ ssm_bwd_kernel(
         for (int s = 0; s < SPG; ++s) {
             d_cur[s] = d_nxt[s];
             y_cur[s] = y_nxt[s];
-            if constexpr (XF) dd_cur[s] = dd_nxt[s];
+            if constexpr (XD) dd_cur[s] = dd_nxt[s];
         }
         if (more) issue(k - 1);
         // one workgroup-uniform decision per chunk: the clamped path gives the same values whenever
@@ -658,7 +674,7 @@ ssm_bwd_kernel(
                 const float s1 = s_out[0][sg * SPG + s][lc];
                 buf_st<T>(rdu, lofs + s * row_bytes, __builtin_fmaf(Dl, y_cur[s], d_cur[s] * s1));
                 float dd = s_out[1][sg * SPG + s][lc];
-                if constexpr (XF) {
+                if constexpr (XD) {
                     dd *= dd_cur[s];  // through softplus (1 without it)
                     if (t0 + sg * SPG + s < L) dbias_acc += dd;
                 }
@@ -683,7 +699,7 @@ ssm_bwd_kernel(
         stv<SPL>(dA_part + (pr * D + d) * NS + n0, dAacc);
     }
     {  // dD (and delta_bias) partials: the NSG loader threads of a channel, in order
-        const bool with_bias = XF && xf.delta_bias != nullptr;
+        const bool with_bias = XD && xf.delta_bias != nullptr;
         __syncthreads();
         float* red = &s_out[0][0][0];  // free after the chunk loop; 2*NSG*CPB <= 2*TC*OS floats
         red[sg * CPB + lc] = dDl;
@@ -777,7 +793,7 @@ int bwd_groups(const SsmShape& s, int ns, int spl) {
     return (int)((s.dim + cpb - 1) / cpb);
 }
 
-template <typename T, int NS, int SPL, bool XF>
+template <typename T, int NS, int SPL, int XF>
 static hipError_t bwd_inst(const BwdArgs& a, const SsmShape& s, hipStream_t st) {
     const int nblk_d = bwd_groups(s, NS, SPL);
     const int nck = (int)((s.seqlen + kCkptSteps - 1) / kCkptSteps);
@@ -797,8 +813,13 @@ static hipError_t bwd_inst(const BwdArgs& a, const SsmShape& s, hipStream_t st) 
 
 template <typename T, int NS, int SPL>
 static hipError_t bwd_inst(const BwdArgs& a, const SsmShape& s, hipStream_t st) {
-    const bool xf = a.xf.delta_bias != nullptr || a.xf.softplus || a.xf.z != nullptr;
-    return xf ? bwd_inst<T, NS, SPL, true>(a, s, st) : bwd_inst<T, NS, SPL, false>(a, s, st);
+    const int xf = (a.xf.delta_bias != nullptr || a.xf.softplus ? kXfDelta : 0) | (a.xf.z != nullptr ? kXfGate : 0);
+    switch (xf) {
+        case 0: return bwd_inst<T, NS, SPL, 0>(a, s, st);
+        case kXfDelta: return bwd_inst<T, NS, SPL, kXfDelta>(a, s, st);
+        case kXfGate: return bwd_inst<T, NS, SPL, kXfGate>(a, s, st);
+        default: return bwd_inst<T, NS, SPL, kXfDelta | kXfGate>(a, s, st);
+    }
 }
 
 hipError_t launch_ssm_bwd(int dt, int ns, int spl, const BwdArgs& a, const SsmShape& s, hipStream_t st) {

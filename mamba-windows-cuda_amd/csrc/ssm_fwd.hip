@@ -73,9 +73,8 @@ __device__ __forceinline__ void vst(float* p, const float (&v)[K]) {
 
 enum FwdMode { kMain = 0, kState = 1, kCarry = 2 };
 
-// XF: the elementwise transforms of ScanXf are compiled in (the plain scan does not carry their
-// registers).
-template <typename T, int NS, int SPL, int MODE, bool XF>
+// XF: the transforms of ScanXf compiled in (kXfDelta, kXfGate bits; the gate only with an output).
+template <typename T, int NS, int SPL, int MODE, int XF>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == 2 ? carry_min_waves(SPL) : fwd_min_waves(SPL), 8)))
 ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __restrict__ A,
                const T* __restrict__ Bm, const T* __restrict__ Cm, const T* __restrict__ Dv,
@@ -162,8 +161,9 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
     const uint32_t lofs = lvalid ? ((uint32_t)(sg * SPG) * (uint32_t)D + (uint32_t)ld_d) * sizeof(T) : kOob;
     const uint32_t row_bytes = (uint32_t)D * sizeof(T);
     auto chunk_rows = [&](int k) { return (uint32_t)min(TC, L - k * TC); };
-    // z is read only when the gated output is stored
-    const T* zb = XF && HAS_OUT && xf.z && out_z ? static_cast<const T*>(xf.z) + row0 * D : nullptr;
+    // z is read only when the gated output is stored (the launcher sets kXfGate only with z and out_z)
+    constexpr bool XD = (XF & kXfDelta) != 0, XG = HAS_OUT && (XF & kXfGate) != 0;
+    const T* zb = XG ? static_cast<const T*>(xf.z) + row0 * D : nullptr;
     T pu[SPG], pd[SPG], pz[SPG], pb[BCPT], pc[BCPT];
     auto issue = [&](int k) {
         const int64_t ck = (int64_t)k * TC;
@@ -175,7 +175,7 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
             pu[s] = buf_raw<T>(ru, lofs + s * row_bytes);
             pd[s] = buf_raw<T>(rd, lofs + s * row_bytes);
         }
-        if (XF && zb != nullptr) {
+        if constexpr (XG) {
             const rsrc_t rz = make_rsrc(zb + ck * D, rows * row_bytes);
 #pragma unroll
             for (int s = 0; s < SPG; ++s) pz[s] = buf_raw<T>(rz, lofs + s * row_bytes);
@@ -192,26 +192,34 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
     // loader thread also stores those outputs, so the consumer lanes never touch u
     const float Dl = HAS_OUT ? ld(Dv + ld_d) : 0.f;
     // delta' = softplus(delta + bias): applied once per element here; rows past L stay 0
-    const bool xform = XF && (xf.delta_bias != nullptr || xf.softplus);
-    const float lbias = XF && xf.delta_bias ? ld(static_cast<const T*>(xf.delta_bias) + ld_d) : 0.f;
+    const float lbias = XD && xf.delta_bias ? ld(static_cast<const T*>(xf.delta_bias) + ld_d) : 0.f;
     float du_cur[SPG], du_nxt[SPG], gz_cur[SPG], gz_nxt[SPG];
     auto commit = [&](int k, int buf) {
         float vd[SPG], vdu[SPG];
         float vmax = 0.f;
 #pragma unroll
-        for (int s = 0; s < SPG; ++s) {
-            vd[s] = static_cast<float>(pd[s]);
-            if (XF && xform) {
-                vd[s] += lbias;
-                if (xf.softplus) vd[s] = softplus_f(vd[s]);
-                if (k * TC + sg * SPG + s >= L) vd[s] = 0.f;
+        for (int s = 0; s < SPG; ++s) vd[s] = static_cast<float>(pd[s]);
+        if constexpr (XD) {
+#pragma unroll
+            for (int s = 0; s < SPG; ++s) vd[s] += lbias;  // 0 without a bias
+            if (xf.softplus) {
+#pragma unroll
+                for (int s = 0; s < SPG; ++s) vd[s] = softplus_f(vd[s]);
             }
+            if ((k + 1) * TC > L) {  // the ragged last chunk: padded steps keep delta' = 0
+#pragma unroll
+                for (int s = 0; s < SPG; ++s)
+                    if (k * TC + sg * SPG + s >= L) vd[s] = 0.f;
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < SPG; ++s) {
             vmax = __builtin_fmaxf(vmax, __builtin_fabsf(vd[s]));
             if constexpr (CARRY) sdt_l += vd[s];
             const float vu = static_cast<float>(pu[s]);
             vdu[s] = vd[s] * vu;
             du_nxt[s] = Dl * vu;
-            if (XF && zb != nullptr) {
+            if constexpr (XG) {
                 const float zv = static_cast<float>(pz[s]);
                 gz_nxt[s] = zv * sigmoid_f(zv);  // silu(z)
             }
@@ -251,7 +259,7 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
 #pragma unroll
         for (int s = 0; s < SPG; ++s) {
             du_cur[s] = du_nxt[s];
-            if constexpr (XF) gz_cur[s] = gz_nxt[s];
+            if constexpr (XG) gz_cur[s] = gz_nxt[s];
         }
         if (more) issue(k + 1);
         if (ckb != nullptr && valid) vst<SPL>(ckb + (int64_t)k * D * NS, h);
@@ -335,12 +343,12 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
             // the loader's (channel, steps) outputs: y from the tile plus D*u
             const uint32_t obytes = chunk_rows(k) * row_bytes;
             const rsrc_t ro = make_rsrc(ob + (int64_t)k * TC * D, ob != nullptr ? obytes : 0);
-            const rsrc_t rz = make_rsrc(out_z + row0 * D + (int64_t)k * TC * D, XF && zb != nullptr ? obytes : 0);
+            const rsrc_t rz = make_rsrc(out_z + row0 * D + (int64_t)k * TC * D, XG ? obytes : 0);
 #pragma unroll
             for (int s = 0; s < SPG; ++s) {
                 const float y = s_y[buf][sg * SPG + s][lc] + du_cur[s];
                 buf_st<T>(ro, lofs + s * row_bytes, y);  // size 0 when out is not wanted: dropped
-                if (XF && zb != nullptr) buf_st<T>(rz, lofs + s * row_bytes, y * gz_cur[s]);
+                if constexpr (XG) buf_st<T>(rz, lofs + s * row_bytes, y * gz_cur[s]);
             }
         }
     }
@@ -364,7 +372,7 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
     }
 }
 
-template <typename T, int NS, int SPL, int MODE, bool XF>
+template <typename T, int NS, int SPL, int MODE, int XF>
 static void fwd_launch(const FwdArgs& a, const SsmShape& s, int nseg_launched, hipStream_t st) {
     constexpr int CPB = 4 * 64 / (NS / SPL);
     const int nblk_d = (int)((s.dim + CPB - 1) / CPB);
@@ -377,20 +385,28 @@ static void fwd_launch(const FwdArgs& a, const SsmShape& s, int nseg_launched, h
                        a.ncar, a.cfold, a.xf, (T*)a.out_z);
 }
 
-template <typename T, int NS, int SPL, bool XF>
+template <typename T, int NS, int SPL, int XF>
 static hipError_t fwd_inst(const FwdArgs& a, const SsmShape& s, hipStream_t st) {
-    if (a.nseg > 1) fwd_launch<T, NS, SPL, kCarry, XF>(a, s, a.ncar, st);  // carries of all chunks before the last segment
+    // the state-only passes see only the delta transform
+    if (a.nseg > 1) fwd_launch<T, NS, SPL, kCarry, XF & kXfDelta>(a, s, a.ncar, st);  // carries of all chunks before the last segment
     if (a.out != nullptr || a.out_z != nullptr)
         fwd_launch<T, NS, SPL, kMain, XF>(a, s, a.nseg, st);
     else
-        fwd_launch<T, NS, SPL, kState, XF>(a, s, a.nseg, st);
+        fwd_launch<T, NS, SPL, kState, XF & kXfDelta>(a, s, a.nseg, st);
     return hipGetLastError();
 }
 
 template <typename T, int NS, int SPL>
 static hipError_t fwd_inst(const FwdArgs& a, const SsmShape& s, hipStream_t st) {
-    const bool xf = a.xf.delta_bias != nullptr || a.xf.softplus || a.xf.z != nullptr;
-    return xf ? fwd_inst<T, NS, SPL, true>(a, s, st) : fwd_inst<T, NS, SPL, false>(a, s, st);
+    // the gate applies only to the gated output (z without out_z is unused)
+    const int xf = (a.xf.delta_bias != nullptr || a.xf.softplus ? kXfDelta : 0) |
+                   (a.xf.z != nullptr && a.out_z != nullptr ? kXfGate : 0);
+    switch (xf) {
+        case 0: return fwd_inst<T, NS, SPL, 0>(a, s, st);
+        case kXfDelta: return fwd_inst<T, NS, SPL, kXfDelta>(a, s, st);
+        case kXfGate: return fwd_inst<T, NS, SPL, kXfGate>(a, s, st);
+        default: return fwd_inst<T, NS, SPL, kXfDelta | kXfGate>(a, s, st);
+    }
 }
 
 hipError_t launch_ssm_fwd(int dt, int ns, int spl, const FwdArgs& a, const SsmShape& s, hipStream_t st) {

@@ -168,6 +168,32 @@ def test_fused_transforms(dev, monkeypatch, xf, dtype, shape, nseg):
         _close("dz", gr["z"], r["dz"], dtype)
 
 
+def test_fused_transforms_wide_delta(dev, monkeypatch):
+    """softplus over its whole range: raw delta + bias from about -40 to +35, so every branch of the
+    kernels' softplus (x itself above 20, the log2 form, the series for e^x < 2^-6) and the
+    derivative past the threshold are taken; fp32, L split into segments, ragged last chunk."""
+    monkeypatch.setenv("MWC_NSEG", "3")
+    B, L, D = 2, 203, 96
+    x = workloads.ssm_inputs(B, L, D, dtype=torch.float32, h_prev=True, seed=31)
+    g = torch.Generator().manual_seed(11)
+    x["delta"] = -4.0 + 9.0 * torch.randn(B, L, D, generator=g)
+    x["delta_bias"] = 0.5 * torch.randn(D, generator=g)
+    x["z"] = torch.randn(B, L, D, generator=g)
+    pre = x["delta"] + x["delta_bias"]
+    assert (pre > 20).any() and (pre < -10).any()
+    dhl = 0.5 * torch.randn(B, D, 16, generator=g)
+    out, h_last, gr = _run_xf(x, dev, bias=True, softplus=True, gate=True, dh_last=dhl)
+    kw = dict(delta_bias=x["delta_bias"], delta_softplus=True, z=x["z"], clamp=True)
+    ro, rh, _ = orc.ssm_fwd_xf(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["h_prev"], **kw)
+    _close("out", out, ro, torch.float32)
+    _close("h_last", h_last, rh, torch.float32)
+    r = orc.ssm_bwd_xf(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["dout"], x["h_prev"], dhl, **kw)
+    for k, name in GRADS + (("h_prev", "dh_prev"),):
+        _close(name, gr[k], r[name], torch.float32)
+    _close("ddelta_bias", gr["delta_bias"], r["ddelta_bias"], torch.float32)
+    _close("dz", gr["z"], r["dz"], torch.float32)
+
+
 def test_fused_transforms_levels_agree(dev):
     """Checkpoint levels 0 and 1 give bitwise-equal results with all three transforms."""
     x = workloads.ssm_inputs(2, 300, 96, dtype=torch.float32, h_prev=True, seed=9)
