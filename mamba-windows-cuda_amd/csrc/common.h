@@ -78,6 +78,25 @@ template <> __device__ __forceinline__ void buf_st<half_t>(rsrc_t r, uint32_t of
 template <> __device__ __forceinline__ void buf_st<bf16_t>(rsrc_t r, uint32_t off, float v) {
     __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, static_cast<bf16_t>(v)), r, off, 0, 0);
 }
+// K consecutive fp32 values (K = 1, 2 or a multiple of 4) as 4-, 8- or 16-byte buffer stores.
+template <int K> __device__ __forceinline__ void buf_st_f32(rsrc_t r, uint32_t off, const float (&v)[K]) {
+    typedef int v2i __attribute__((ext_vector_type(2)));
+    typedef int v4i __attribute__((ext_vector_type(4)));
+    if constexpr (K == 1) {
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, v[0]), r, off, 0, 0);
+    } else if constexpr (K == 2) {
+        const v2i q = {__builtin_bit_cast(int, v[0]), __builtin_bit_cast(int, v[1])};
+        __builtin_amdgcn_raw_buffer_store_b64(q, r, off, 0, 0);
+    } else {
+        static_assert(K % 4 == 0, "vector width");
+#pragma unroll
+        for (int k = 0; k < K; k += 4) {
+            const v4i q = {__builtin_bit_cast(int, v[k]), __builtin_bit_cast(int, v[k + 1]),
+                           __builtin_bit_cast(int, v[k + 2]), __builtin_bit_cast(int, v[k + 3])};
+            __builtin_amdgcn_raw_buffer_store_b128(q, r, off + 4 * k, 0, 0);
+        }
+    }
+}
 
 // Elementwise transforms around the scan, from the hardware base-2 exp/log and reciprocal
 // (each ~1 ulp). softplus(x) = ln(1 + e^x): x itself above 20 (as torch's threshold), the series

@@ -113,7 +113,8 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
     __shared__ __align__(16) float s_in[2][2][CPB][RS];  // [buf][delta, dout][channel][step]
     __shared__ __align__(16) float s_c[2][TC][NS];
     // per staging buffer: the index of the last chunk staged there whose exponents can reach the clamp
-    __shared__ int s_flag[2];
+    // ([2], [3]: sinks for the loaders' writes of the chunks that cannot)
+    __shared__ int s_flag[4];
 
     const int tid = threadIdx.x;
     const int lid = xcd_remap(blockIdx.x, gridDim.x);
@@ -203,7 +204,7 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
             vmax = __builtin_fmaxf(vmax, __builtin_fabsf(vd[s]));
             sdt_l += vd[s];
         }
-        if (vmax * lamax2 > kExp2Clamp) s_flag[buf] = k;  // benign race: every writer stores k
+        s_flag[vmax * lamax2 > kExp2Clamp ? buf : 2 + buf] = k;  // branch-free: flag word or sink, all store k
         stv<SPG>(&s_in[buf][0][lc][sg * SPG], vd);
         stv<SPG>(&s_in[buf][1][lc][sg * SPG], vy);
 #pragma unroll
@@ -323,7 +324,7 @@ ssm_bwd_kernel(
     auto s_in = [&](int plane, int ch) -> float* { return &s_in_raw[plane * AS + ch * RS]; };
     __shared__ __align__(16) float s_part[4][TC][2 * NS];
     __shared__ __align__(16) float s_out[2][TC][OS];  // [du, ddelta][step][channel]
-    __shared__ int s_flag;              // index of the last staged chunk that needs the exponent clamp
+    __shared__ int s_flag[2];  // [0]: index of the last staged chunk that needs the exponent clamp; [1]: sink
 
     const int tid = threadIdx.x;
     const int lid = xcd_remap(blockIdx.x, gridDim.x);
@@ -473,7 +474,7 @@ ssm_bwd_kernel(
 #pragma unroll
             for (int s = 0; s < SPG; ++s) buf_st<T>(rdz, lofs + s * row_bytes, vdz[s]);
         }
-        if (vmax * lamax2 > kExp2Clamp) s_flag = k;  // benign race: every writer stores k
+        s_flag[vmax * lamax2 > kExp2Clamp ? 0 : 1] = k;  // branch-free: flag word or sink, all store k
         stv<SPG>((s_in(0, lc) + sg * SPG), vd);
         stv<SPG>((s_in(1, lc) + sg * SPG), vdu);
         stv<SPG>((s_in(2, lc) + sg * SPG), vu);
@@ -491,7 +492,7 @@ ssm_bwd_kernel(
     };
 
     float hin[SPL];
-    if (tid == 0) s_flag = -1;
+    if (tid == 0) s_flag[0] = -1;
     __syncthreads();
     if (k0 < k1) {  // L == 0 has no chunk; the outputs below are then dh_prev = dh_last and zero partials
         issue(k1 - 1);
@@ -516,7 +517,7 @@ ssm_bwd_kernel(
         if (more) issue(k - 1);
         // one workgroup-uniform decision per chunk: the clamped path gives the same values whenever
         // no exponent reaches the clamp, so deciding for the whole workgroup is exact
-        const bool need_clamp = __builtin_amdgcn_readfirstlane(s_flag) == k;
+        const bool need_clamp = __builtin_amdgcn_readfirstlane(s_flag[0]) == k;
 
         // ---- recompute the chunk's states (one exp per state), 4 steps per operand read ----
         float H[TC][SPL], E[TC][SPL];
@@ -681,11 +682,22 @@ ssm_bwd_kernel(
                 buf_st<T>(rdd, lofs + s * row_bytes, dd);
             }
         }
-        // this workgroup's dB/dC partial for the chunk (sum of its 4 waves)
-        for (int o = tid; o < TC * 2 * NS; o += 256) {
-            const int tt = o / (2 * NS), v = o % (2 * NS);
-            const float s = s_part[0][tt][v] + s_part[1][tt][v] + s_part[2][tt][v] + s_part[3][tt][v];
-            if (t0 + tt < L) dbc_part[(((int64_t)blk * Bsz + b) * L + t0 + tt) * (2 * NS) + v] = s;
+        {  // this workgroup's dB/dC partial for the chunk (sum of its 4 waves), PV consecutive values
+           // per thread; the buffer spans the chunk's rows before L, so the stores of later rows drop
+            constexpr int PV = TC * 2 * NS / 256;
+            static_assert(PV * 256 == TC * 2 * NS && (PV <= 2 || PV % 4 == 0), "partial tiling");
+            const int o = tid * PV, tt = o / (2 * NS), v = o % (2 * NS);
+            float acc[PV], w[PV];
+            ldv<PV>(&s_part[0][tt][v], acc);
+#pragma unroll
+            for (int q = 1; q < 4; ++q) {
+                ldv<PV>(&s_part[q][tt][v], w);
+#pragma unroll
+                for (int p = 0; p < PV; ++p) acc[p] += w[p];
+            }
+            const rsrc_t rp = make_rsrc(dbc_part + (((int64_t)blk * Bsz + b) * L + t0) * (2 * NS),
+                                        chunk_rows(k) * 2 * NS * sizeof(float));
+            buf_st_f32<PV>(rp, o * sizeof(float), acc);
         }
         __syncthreads();  // the next chunk's tile is staged; s_out / s_part are free again
     }
