@@ -98,6 +98,30 @@ template <int K> __device__ __forceinline__ void buf_st_f32(rsrc_t r, uint32_t o
     }
 }
 
+// Issue priority by progress through a workgroup's chunks. A SIMD's arbiter issues from the
+// highest-priority ready wave and, among equals, from the oldest, so workgroups that share a CU and
+// start together would finish in dispatch order, far apart (the fused backward at 3 workgroups per
+// CU: 210, 253 and 302 us), and the last would run alone at a fraction of the CU's throughput.
+// Dropping a wave's priority as it passes 1/2, 3/4 and 7/8 of its chunks lets the ones behind
+// catch up, so they finish close together.
+struct ProgressPrio {
+    int b1, b2, b3;  // chunks done at which the priority drops to 2, 1, 0
+    __device__ __forceinline__ explicit ProgressPrio(int nchunks)
+        : b1(nchunks / 2), b2(3 * nchunks / 4), b3(7 * nchunks / 8) {
+        __builtin_amdgcn_s_setprio(3);
+    }
+    __device__ __forceinline__ void update(int done) {
+        if (done == b1 || done == b2 || done == b3) {
+            if (done == b3)
+                __builtin_amdgcn_s_setprio(0);
+            else if (done == b2)
+                __builtin_amdgcn_s_setprio(1);
+            else
+                __builtin_amdgcn_s_setprio(2);
+        }
+    }
+};
+
 // Elementwise transforms around the scan, from the hardware base-2 exp/log and reciprocal
 // (each ~1 ulp). softplus(x) = ln(1 + e^x): x itself above 20 (as torch's threshold), the series
 // t - t^2/2 + t^3/3 for t = e^x < 2^-6 (where 1 + t would round away t's low bits; the first

@@ -221,9 +221,11 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
         commit(k1 - 1, (k1 - 1) & 1);
     }
     __syncthreads();
+    ProgressPrio prio(k1 - k0);
     for (int k = k1 - 1; k >= k0; --k) {
         const int buf = k & 1;
         const bool more = k > k0;
+        prio.update(k1 - 1 - k);
         if (more) issue(k - 1);
         // operands are read four steps at a time, which keeps the pass to few enough registers for
         // twice the waves per SIMD (its chunks are short on arithmetic, so more waves in flight are
@@ -505,9 +507,11 @@ ssm_bwd_kernel(
     float* red_g = &s_red[wave][0];   // [slot][channel][16]
     float* red_h = &s_red[wave][PL];  // [slot][channel][16]
 
+    ProgressPrio prio(k1 - k0);
     for (int k = k1 - 1; k >= k0; --k) {
         const int t0 = k * TC;
         const bool more = k > k0;
+        prio.update(k1 - 1 - k);
 #pragma unroll
         for (int s = 0; s < SPG; ++s) {
             d_cur[s] = d_nxt[s];

@@ -253,9 +253,11 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
     float* ckb = (!CARRY && ckpt) ? ckpt + ((int64_t)b * nck * D + d) * NS + n0 : nullptr;
     T* ob = HAS_OUT && out != nullptr ? out + row0 * D : nullptr;
 
+    ProgressPrio prio(k1 - k0);
     for (int k = k0; k < k1; ++k) {
         const int buf = k & 1;
         const bool more = k + 1 < k1;
+        prio.update(k - k0);
 #pragma unroll
         for (int s = 0; s < SPG; ++s) {
             du_cur[s] = du_nxt[s];
