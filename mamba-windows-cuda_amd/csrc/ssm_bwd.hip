@@ -583,9 +583,23 @@ ssm_bwd_kernel(
                     if constexpr (LPI >= 2) acc[q] += dpp<kDppXor1>(acc[q]);
                     if constexpr (LPI >= 4) acc[q] += dpp<kDppXor2>(acc[q]);
                 }
-                // combine in every lane, ahead of the store's lane mask, so each DPP move fuses into its add
-                asm("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]));
-                if (rsub == 0) stv<4>(&s_part[wave][phase * kRedSlots + rs][rq * 4], acc);
+                float* const dst = &s_part[wave][phase * kRedSlots + rs][rq * 4];
+                if constexpr (LPI == 1) {
+                    stv<4>(dst, acc);
+                } else {
+                    // every lane of the group holds the 4 sums: each writes its 4/LPI of them (narrow
+                    // LDS writes cost less than one 16-byte write by one lane)
+                    constexpr int W = 4 / LPI;
+                    float w[W];
+#pragma unroll
+                    for (int q = 0; q < W; ++q) {
+                        if constexpr (LPI == 2)
+                            w[q] = rsub ? acc[2 + q] : acc[q];
+                        else
+                            w[q] = (rsub & 2) ? ((rsub & 1) ? acc[3] : acc[2]) : ((rsub & 1) ? acc[1] : acc[0]);
+                    }
+                    stv<W>(dst + rsub * W, w);
+                }
             }
         };
         {
