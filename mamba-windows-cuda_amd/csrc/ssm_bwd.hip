@@ -16,7 +16,7 @@
 // in reverse in chunks of 16 steps; each chunk restarts from the fp32
 // checkpoint the forward stored, recomputes the chunk's states and decay
 // factors into VGPRs (one exp per state) and runs the reverse sweep. Inputs
-// are staged through LDS as in the forward (fp32 delta, delta*u, u, dout rows
+// are staged through LDS as in the forward (fp32 delta, delta*u, dout rows
 // per channel; B/C rows per step); the previous chunk's global loads are in
 // flight during the sweep and land in LDS between the chunk's two barriers.
 // Sums over n (du, ddelta) are DPP reductions inside the lane group. Sums over
@@ -313,10 +313,10 @@ ssm_bwd_kernel(
     constexpr int QPL = NQ <= 16 ? 1 : NQ / 16;
     static_assert(NSG * SPG == TC && CPW >= LPI && (BCN < 256 || BCN % 256 == 0) && LPI <= 4, "tiling");
 
-    // [delta, delta*u, u, dout] planes of [channel][step]; planes are AS floats apart
+    // [delta, delta*u, dout] planes of [channel][step]; planes are AS floats apart
     // (AS = 16 mod 64 banks) so the delta*u and dout weights of one channel sit in different banks
     constexpr int AS = CPB * RS + 16;
-    __shared__ __align__(16) float s_in_raw[4 * AS];
+    __shared__ __align__(16) float s_in_raw[3 * AS];
     // B/C rows of the chunk, [step][n / SPL][B x SPL, C x SPL]: a lane reads its B and C with one access
     __shared__ __align__(16) float s_bc[TC][2 * NS];
     // wave-private slabs of g_t (plane 0) and h_t (plane 1): [wave][plane][slot][channel][16];
@@ -427,7 +427,7 @@ ssm_bwd_kernel(
     // dout (as the scan sees them), for du = D*dout + delta*sum_n g*B; dD accumulates here, once per
     // element
     const float Dl = ld(Dv + ld_d);
-    float d_cur[SPG], d_nxt[SPG], y_cur[SPG], y_nxt[SPG];
+    float d_cur[SPG], d_nxt[SPG], y_cur[SPG], y_nxt[SPG], u_cur[SPG], u_nxt[SPG];
     float dDl = 0.f;
     auto commit = [&](int k) {
         float vd[SPG], vdu[SPG], vu[SPG], vy[SPG];
@@ -469,6 +469,7 @@ ssm_bwd_kernel(
             vmax = __builtin_fmaxf(vmax, __builtin_fabsf(vd[s]));
             d_nxt[s] = vd[s];
             y_nxt[s] = vy[s];
+            u_nxt[s] = vu[s];
             dDl = __builtin_fmaf(vy[s], vu[s], dDl);  // rows past L read as 0
         }
         if constexpr (XG) {  // dz = dout * out * silu'(z) needs no scan: store it now
@@ -479,8 +480,7 @@ ssm_bwd_kernel(
         s_flag[vmax * lamax2 > kExp2Clamp ? 0 : 1] = k;  // branch-free: flag word or sink, all store k
         stv<SPG>((s_in(0, lc) + sg * SPG), vd);
         stv<SPG>((s_in(1, lc) + sg * SPG), vdu);
-        stv<SPG>((s_in(2, lc) + sg * SPG), vu);
-        stv<SPG>((s_in(3, lc) + sg * SPG), vy);
+        stv<SPG>((s_in(2, lc) + sg * SPG), vy);
 #pragma unroll
         for (int q = 0; q < BCPT; ++q) {
             const int e = tid * BCPT + q;
@@ -515,6 +515,7 @@ ssm_bwd_kernel(
 #pragma unroll
         for (int s = 0; s < SPG; ++s) {
             d_cur[s] = d_nxt[s];
+            u_cur[s] = u_nxt[s];
             y_cur[s] = y_nxt[s];
             if constexpr (XD) dd_cur[s] = dd_nxt[s];
         }
@@ -566,7 +567,7 @@ ssm_bwd_kernel(
                 const int rq = rq0 + qq;
                 const bool is_c = rq >= NQ / 2;
                 const float* plane = is_c ? red_h : red_g;
-                const float* wrow = s_in(is_c ? 3 : 1, wave * CPW) + phase * kRedSlots + rs;
+                const float* wrow = s_in(is_c ? 2 : 1, wave * CPW) + phase * kRedSlots + rs;
                 const int q4 = (rq % (NQ / 2)) * 4;
                 float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -603,16 +604,16 @@ ssm_bwd_kernel(
             }
         };
         {
-            float uq[4], yq[4], dq[4], uqn[4], yqn[4], dqn[4], Bn[SPL], Cn[SPL];
-            // The group sums over n of each step, S1 = sum g*B (for du) and S2 = sum g*(A*dA*h_{t-1} +
-            // u*B) (= ddelta), are reduce-scattered over the group every RST steps: the lane's partials of
+            float yq[4], dq[4], yqn[4], dqn[4], Bn[SPL], Cn[SPL];
+            // The group sums over n of each step, S1 = sum g*B (for du) and S2 = sum g*A*dA*h_{t-1} (with
+            // u*S1, ddelta), are reduce-scattered over the group every RST steps: the lane's partials of
             // RST steps x (S1, S2) go in, and the lane writes the one (step, sum) the scatter leaves it.
+            // The storing threads add u*S1 once per element.
             constexpr int RV = LPC, RST = RV / 2;
             float rp[RV];
             const int ridx = rs_index<LPC, RV>(lane);
             float* const s_mine = &s_out[ridx & 1][ridx >> 1][c];  // + the round's first step * OS
-            ldv<4>(s_in(2, c) + TC - 4, uqn);
-            ldv<4>(s_in(3, c) + TC - 4, yqn);
+            ldv<4>(s_in(2, c) + TC - 4, yqn);
             ldv<4>(s_in(0, c) + TC - 4, dqn);
             auto ld_bc = [&](int i, float (&Bo)[SPL], float (&Co)[SPL]) {
                 float bc[2 * SPL];
@@ -630,13 +631,11 @@ ssm_bwd_kernel(
                 if (slot == kRedSlots - 1) {
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
-                        uq[q] = uqn[q];
                         yq[q] = yqn[q];
                         dq[q] = dqn[q];
                     }
                     if (i >= 4) {
-                        ldv<4>(s_in(2, c) + i - 7, uqn);
-                        ldv<4>(s_in(3, c) + i - 7, yqn);
+                        ldv<4>(s_in(2, c) + i - 7, yqn);
                         ldv<4>(s_in(0, c) + i - 7, dqn);
                     }
                 }
@@ -652,7 +651,7 @@ ssm_bwd_kernel(
                 // keep the next step's operand reads here, a full step ahead of their use (the
                 // scheduler would otherwise sink them next to the use and expose the LDS latency)
                 __builtin_amdgcn_sched_barrier(0);
-                const float ui = uq[slot], yo = yq[slot], dti = dq[slot];
+                const float yo = yq[slot], dti = dq[slot];
                 float gt[SPL];
                 float r1 = 0.f, r2 = 0.f;
 #pragma unroll
@@ -666,7 +665,7 @@ ssm_bwd_kernel(
                     dAacc[j] = __builtin_fmaf(dti, s, dAacc[j]);
                 }
                 rp[2 * (i % RST)] = r1;
-                rp[2 * (i % RST) + 1] = __builtin_fmaf(ui, r1, r2);
+                rp[2 * (i % RST) + 1] = r2;
                 if (i % RST == 0) s_mine[i * OS] = reduce_scatter<LPC, RV>(rp, lane);
                 const int sl = slot * CPW + cw;
                 stv<SPL>(red_g + sl * NS + n0, gt);
@@ -692,7 +691,7 @@ ssm_bwd_kernel(
             for (int s = 0; s < SPG; ++s) {
                 const float s1 = s_out[0][sg * SPG + s][lc];
                 buf_st<T>(rdu, lofs + s * row_bytes, __builtin_fmaf(Dl, y_cur[s], d_cur[s] * s1));
-                float dd = s_out[1][sg * SPG + s][lc];
+                float dd = __builtin_fmaf(u_cur[s], s1, s_out[1][sg * SPG + s][lc]);  // + u * S1
                 if constexpr (XD) {
                     dd *= dd_cur[s];  // through softplus (1 without it)
                     if (t0 + sg * SPG + s < L) dbias_acc += dd;
