@@ -130,7 +130,7 @@ def _run_xf(x, dev, *, bias, softplus, gate, lvl=0, dh_last=None):
     return out, h_last, {k: v.grad for k, v in leaves.items()}
 
 
-XF_CASES = [(True, True, True), (True, True, False), (False, False, True), (False, True, False)]
+XF_CASES = [(True, True, True), (True, True, False), (False, False, True), (False, True, False), (True, False, False)]
 
 
 @pytest.mark.parametrize("xf", XF_CASES)
