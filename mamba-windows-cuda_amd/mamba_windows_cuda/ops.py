@@ -10,6 +10,9 @@ before any device work is queued.
 """
 from __future__ import annotations
 
+import functools
+import os
+
 import torch
 
 from . import _lib
@@ -68,17 +71,20 @@ def _require(cond: bool, msg: str) -> None:
 
 def check_ssm_inputs(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, *, require_device=True):
     """Raise RuntimeError unless the inputs satisfy the reference's contract."""
+    # (messages are formatted only on failure: these checks run on every call)
     named = (("u", u), ("delta", delta), ("A", A), ("B_ssm", B_ssm), ("C_ssm", C_ssm), ("D_ssm", D_ssm))
     if require_device:
         for name, t in named:
-            _require(t.is_cuda, f"{name} must be a CUDA tensor")
+            if not t.is_cuda:
+                raise RuntimeError(f"{name} must be a CUDA tensor")
     # bfloat16 is accepted in addition to the reference's float32/float16 (storage only, fp32 math)
     _require(u.dtype in STORAGE_DTYPES, "u must be float32/float16 (or bfloat16)")
     for name, t in named[1:]:
-        _require(t.dtype == u.dtype, f"{name} dtype must match u dtype")
+        if t.dtype != u.dtype:
+            raise RuntimeError(f"{name} dtype must match u dtype")
     for name, t in named:
-        _require(t.dim() == 0 or t.stride(-1) == 1 or t.size(-1) == 1,
-                 f"{name} must be contiguous in the last dimension")
+        if not (t.dim() == 0 or t.stride(-1) == 1 or t.size(-1) == 1):
+            raise RuntimeError(f"{name} must be contiguous in the last dimension")
     _require(A.dim() == 2, "A must be 2D (dim, state)")
     _require(A.size(1) in NSTATES, "Only N=16 (or 8, 32, 64) is supported")
     n = A.size(1)
@@ -106,8 +112,24 @@ def check_ssm_inputs(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, *, require_d
         _require(h_prev.device == u.device, "h_prev must be on the same device as u")
 
 
+@functools.lru_cache(maxsize=1024)
 def ckpt_count(seqlen: int) -> int:
     return int(_lib.lib().mwc_ssm_ckpt_count(seqlen))
+
+
+# The launch plan (and so the workspace size) depends on the shape and on the MWC_NSEG / MWC_CFOLD /
+# MWC_SPL overrides, which the library reads at call time: the sizes are cached under both.
+_PLAN_ENV = ("MWC_NSEG", "MWC_CFOLD", "MWC_SPL")
+
+
+@functools.lru_cache(maxsize=1024)
+def _workspace_bytes(which: str, bsz: int, L: int, dm: int, n: int, env: tuple) -> int:
+    fn = _lib.lib().mwc_ssm_fwd_workspace_size if which == "fwd" else _lib.lib().mwc_ssm_bwd_workspace_size
+    return int(fn(bsz, L, dm, n))
+
+
+def workspace_bytes(which: str, bsz: int, L: int, dm: int, n: int) -> int:
+    return _workspace_bytes(which, bsz, L, dm, n, tuple(os.environ.get(k) for k in _PLAN_ENV))
 
 
 def check_transforms(u, delta_bias=None, z=None):
@@ -116,9 +138,12 @@ def check_transforms(u, delta_bias=None, z=None):
     for name, t, shape in (("delta_bias", delta_bias, (dm,)), ("z", z, (bsz, L, dm))):
         if t is None:
             continue
-        _require(t.device == u.device, f"{name} must be on the same device as u")
-        _require(t.dtype == u.dtype, f"{name} dtype must match u dtype")
-        _require(tuple(t.shape) == shape, f"{name} shape must be {shape}")
+        if t.device != u.device:
+            raise RuntimeError(f"{name} must be on the same device as u")
+        if t.dtype != u.dtype:
+            raise RuntimeError(f"{name} dtype must match u dtype")
+        if tuple(t.shape) != shape:
+            raise RuntimeError(f"{name} shape must be {shape}")
 
 
 def ssm_forward_xf(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, *, delta_bias=None, delta_softplus=False,
@@ -144,7 +169,7 @@ def ssm_forward_xf(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, *, delta_bias=
     h_last = torch.empty(bsz, dm, n, dtype=u.dtype, device=dev) if want_h_last else None
     ckpt = (torch.empty(bsz, ckpt_count(L), dm, n, dtype=torch.float32, device=dev)
             if want_ckpt else None)
-    nbytes = L_.mwc_ssm_fwd_workspace_size(bsz, L, dm, n)
+    nbytes = workspace_bytes("fwd", bsz, L, dm, n)
     ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
     with _on_device(dev):
         st = L_.mwc_ssm_fwd_ex(_dtype_code(u), _ptr(u), _ptr(delta), _ptr(A), _ptr(B_ssm), _ptr(C_ssm),
@@ -197,7 +222,7 @@ def ssm_backward_xf(u, delta, A, B_ssm, C_ssm, D_ssm, dout, ckpt, dh_last=None, 
     dh_prev = torch.empty(bsz, dm, n, dtype=u.dtype, device=dev) if want_dh_prev else None
     dbias = torch.empty_like(delta_bias) if delta_bias is not None else None
     dz = torch.empty_like(z) if z is not None else None
-    nbytes = L_.mwc_ssm_bwd_workspace_size(bsz, L, dm, n)
+    nbytes = workspace_bytes("bwd", bsz, L, dm, n)
     ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
     with _on_device(dev):
         st = L_.mwc_ssm_bwd_ex(_dtype_code(u), _ptr(u), _ptr(delta), _ptr(A), _ptr(B_ssm), _ptr(C_ssm),
@@ -221,8 +246,10 @@ def ssm_step(u, delta, A, B_ssm, C_ssm, D_ssm, h, *, delta_bias=None, delta_soft
     given, receives h_new and may be h itself (in-place update)."""
     named = (("u", u), ("delta", delta), ("A", A), ("B_ssm", B_ssm), ("C_ssm", C_ssm), ("D_ssm", D_ssm), ("h", h))
     for name, t in named:
-        _require(t.is_cuda, f"{name} must be a CUDA tensor")
-        _require(t.dtype == u.dtype, f"{name} dtype must match u dtype")
+        if not t.is_cuda:
+            raise RuntimeError(f"{name} must be a CUDA tensor")
+        if t.dtype != u.dtype:
+            raise RuntimeError(f"{name} dtype must match u dtype")
     _require(u.dtype in STORAGE_DTYPES, "u must be float32/float16 (or bfloat16)")
     _require(u.dim() == 2, "u must be 2D (batch, dim) for a step")
     bsz, dm = u.shape
@@ -232,8 +259,10 @@ def ssm_step(u, delta, A, B_ssm, C_ssm, D_ssm, h, *, delta_bias=None, delta_soft
                            ("C_ssm", C_ssm, (bsz, n)), ("D_ssm", D_ssm, (dm,)), ("h", h, (bsz, dm, n)),
                            ("delta_bias", delta_bias, (dm,)), ("z", z, (bsz, dm))):
         if t is not None:
-            _require(tuple(t.shape) == shape, f"{name} shape must be {shape}")
-            _require(t.dtype == u.dtype and t.device == u.device, f"{name} must match u's dtype and device")
+            if tuple(t.shape) != shape:
+                raise RuntimeError(f"{name} shape must be {shape}")
+            if t.dtype != u.dtype or t.device != u.device:
+                raise RuntimeError(f"{name} must match u's dtype and device")
     align = 16  # the kernel moves a lane's states as one 16-byte vector
 
     def aligned(t):

@@ -150,6 +150,8 @@ def test_fused_transforms(dev, monkeypatch, xf, dtype, shape, nseg):
     if softplus:  # raw delta around softplus^-1 of the usual range
         x["delta"] = -4.0 + 2.0 * torch.randn(B, L, D, generator=g)
     x["delta_bias"] = 0.5 * torch.randn(D, generator=g)
+    if not softplus:  # without softplus delta + bias must stay a step size (> 0), or the states grow
+        x["delta_bias"] = 0.1 * x["delta_bias"].abs()
     x["z"] = torch.randn(B, L, D, generator=g)
     x = {k: v.to(dtype) for k, v in x.items()}
     dhl = (0.5 * torch.randn(B, D, 16, generator=g)).to(dtype)
