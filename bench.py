@@ -380,8 +380,8 @@ def main():
                     help="profiling driver: fused calls, cfg4b scan and a 1 GiB copy; no timing")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print(json.dumps({"error": "this build measures one GPU only; multi-GPU sharding is design-only "
-                                   "(see DESIGN.md), run with --gpus 1"}))
+        print(json.dumps({"error": "this build measures one GPU only (sharding over GPUs is designed, not "
+                                   "built); run with --gpus 1"}))
         sys.exit(2)
     import torch
 
