@@ -19,7 +19,9 @@
 // are staged through LDS as in the forward (fp32 delta, delta*u, dout rows
 // per channel; B/C rows per step); the previous chunk's global loads are in
 // flight during the sweep and land in LDS between the chunk's two barriers.
-// Sums over n (du, ddelta) are DPP reductions inside the lane group. Sums over
+// Sums over n (S1 = sum g*B and S2 = sum g*A*dA*h_{t-1}) are DPP reduce-scatters
+// inside the lane group; the storing threads finish du = D*dout + delta*S1 and
+// ddelta = S2 + u*S1 once per element. Sums over
 // channels (dB, dC) go through a wave-private LDS slab: each step the lanes
 // deposit g_t and h_t, and every 4 steps the wave folds its channels with one
 // FMA per state against the per-channel weights (delta*u for dB, dout for dC)
@@ -559,7 +561,7 @@ ssm_bwd_kernel(
                 recompute(std::false_type{});
         }
         // ---- reverse sweep ----
-        // B/C are read one step ahead and u/dout one 4-step group ahead of use; every 4 steps the
+        // B/C are read one step ahead and delta/dout one 4-step group ahead of use; every 4 steps the
         // wave folds the phase's deposits over its channels.
         auto fold = [&](int phase) {
 #pragma unroll
