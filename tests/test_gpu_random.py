@@ -1,0 +1,85 @@
+"""Seeded randomized parity sweep of the fused scan against the float64 oracle.
+
+Each case draws its own shape (ragged B, L, D), state count, storage dtype, initial state, fused
+transforms (bias, softplus, z gate in any combination), launch plan (states per lane, segments of L,
+carry split) and checkpoint level from a fixed seed, so the sweep is the same on every run. It
+crosses the combinations the targeted tests cover one axis at a time: out, h_last and every
+gradient (incl. dh_prev, d(delta_bias), dz) must agree with the oracle to the dtype's tolerance.
+"""
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from mamba_windows_cuda import SelectiveScanCuda, workloads
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: dict(rtol=1e-3, atol=1e-4), torch.float16: dict(rtol=1e-2, atol=1e-2),
+       torch.bfloat16: dict(rtol=2e-2, atol=2e-2)}
+GRADS = (("u", "du"), ("delta", "ddelta"), ("A", "dA"), ("B", "dB"), ("C", "dC"), ("D", "dD"))
+# states per lane built for each state count
+SPLS = {8: (1, 2), 16: (1, 2, 4), 32: (2, 4), 64: (4,)}
+NCASES = 40
+
+
+def _case(idx):
+    r = random.Random(9100 + idx)
+    n = r.choice((8, 16, 16, 32, 64))
+    return dict(
+        B=r.randint(1, 4), L=r.choice((1, r.randint(2, 40), r.randint(41, 260))), D=r.randint(1, 600), n=n,
+        dtype=r.choice((torch.float32, torch.float16, torch.bfloat16)), with_h=r.random() < 0.5,
+        bias=r.random() < 0.4, softplus=r.random() < 0.4, gate=r.random() < 0.4,
+        spl=r.choice((None,) + SPLS[n]), nseg=r.choice((None, None, 2, 3, 4)), cfold=r.choice((None, 1, 2)),
+        lvl=r.choice((0, 0, 1)), seed=r.randint(0, 10 ** 6))
+
+
+def _close(name, got, ref, dtype):
+    np.testing.assert_allclose(got.detach().cpu().double().numpy(), ref, err_msg=name, **TOL[dtype])
+
+
+@pytest.mark.parametrize("idx", range(NCASES))
+def test_random_case(dev, monkeypatch, idx):
+    c = _case(idx)
+    print(f"case random idx={idx} {c}", flush=True)
+    for var, key in (("MWC_SPL", "spl"), ("MWC_NSEG", "nseg"), ("MWC_CFOLD", "cfold")):
+        if c[key] is not None:
+            monkeypatch.setenv(var, str(c[key]))
+    B, L, D, n, dtype = c["B"], c["L"], c["D"], c["n"], c["dtype"]
+    x = workloads.ssm_inputs(B, L, D, dtype=torch.float32, h_prev=True, seed=c["seed"], nstate=n)
+    g = torch.Generator().manual_seed(c["seed"] + 1)
+    if c["softplus"]:  # raw delta around softplus^-1 of the usual range
+        x["delta"] = -4.0 + 2.0 * torch.randn(B, L, D, generator=g)
+    # without softplus delta + bias must stay a step size (> 0)
+    x["delta_bias"] = 0.5 * torch.randn(D, generator=g) if c["softplus"] else 0.05 * torch.rand(D, generator=g)
+    x["z"] = torch.randn(B, L, D, generator=g)
+    x["dh_last"] = 0.5 * torch.randn(B, D, n, generator=g)
+    x = {k: v.to(dtype) for k, v in x.items()}
+
+    names = ["u", "delta", "A", "B", "C", "D"] + (["h_prev"] if c["with_h"] else []) \
+        + (["delta_bias"] if c["bias"] else []) + (["z"] if c["gate"] else [])
+    leaves = {k: x[k].to(dev).requires_grad_(True) for k in names}
+    out, h_last = SelectiveScanCuda(checkpoint_lvl=c["lvl"]).forward_with_state(
+        leaves["u"], leaves["delta"], leaves["A"], leaves["B"], leaves["C"], leaves["D"], leaves.get("h_prev"),
+        z=leaves.get("z"), delta_bias=leaves.get("delta_bias"), delta_softplus=c["softplus"])
+    loss = (out.float() * x["dout"].to(dev).float()).sum() + (h_last.float() * x["dh_last"].to(dev).float()).sum()
+    loss.backward()
+    torch.cuda.synchronize()
+
+    hp = x["h_prev"] if c["with_h"] else None
+    kw = dict(delta_bias=x["delta_bias"] if c["bias"] else None, delta_softplus=c["softplus"],
+              z=x["z"] if c["gate"] else None, clamp=True)
+    ro, rh, _ = orc.ssm_fwd_xf(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], hp, **kw)
+    _close("out", out, ro, dtype)
+    _close("h_last", h_last, rh, dtype)
+    r = orc.ssm_bwd_xf(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["dout"], hp, x["dh_last"], **kw)
+    for k, name in GRADS:
+        _close(name, leaves[k].grad, r[name], dtype)
+    if c["with_h"]:
+        _close("dh_prev", leaves["h_prev"].grad, r["dh_prev"], dtype)
+    if c["bias"]:
+        _close("ddelta_bias", leaves["delta_bias"].grad, r["ddelta_bias"], dtype)
+    if c["gate"]:
+        _close("dz", leaves["z"].grad, r["dz"], dtype)
