@@ -50,6 +50,29 @@ def _traffic_from_profiles(name):
     return float(m.group(1)) if m else None
 
 
+# The GPU's clocks ramp over the first ~0.1 s of sustained load (measured at cfg2: 20 timed steps right
+# after 5 warm-up steps read 0.495 ms per step, 400 read 0.413 ms, the sum of the two calls' times), and a
+# training loop runs at the ramped clock: the warm-up runs its W steps and, past them, until this much
+# wall time of back-to-back steps has passed.
+MIN_WARMUP_S = 0.3
+
+
+def _warmup(fn, n):
+    """Runs `fn` untimed at least `n` times and at least MIN_WARMUP_S of wall time (synchronizing every 16
+    calls, so the time counts work done, not work queued); returns the number of calls run."""
+    import torch
+
+    t0 = time.perf_counter()
+    done = 0
+    while done < n or time.perf_counter() - t0 < MIN_WARMUP_S:
+        fn()
+        done += 1
+        if done % 16 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return done
+
+
 def _events_ms(fn, n):
     import torch
 
@@ -87,16 +110,17 @@ def bench_ssm(cfg, steps, warmup, level, shard=1):
         out = m(leaves["u"], leaves["delta"], leaves["A"], leaves["B"], leaves["C"], leaves["D"])
         torch.autograd.backward(out, dout)
 
-    for _ in range(warmup):
-        step()
+    # activation memory a forward keeps for its backward at this checkpoint level (probed before the
+    # warm-up, so the timed steps follow it with the allocator settled and the clocks ramped)
+    step()
     torch.cuda.synchronize()
-    # activation memory a forward keeps for its backward at this checkpoint level
     base = torch.cuda.memory_allocated()
     out_keep = m(leaves["u"], leaves["delta"], leaves["A"], leaves["B"], leaves["C"], leaves["D"])
     torch.cuda.synchronize()
     kept = torch.cuda.memory_allocated() - base - out_keep.numel() * out_keep.element_size()
     del out_keep
     torch.cuda.reset_peak_memory_stats()
+    warm_run = _warmup(step, warmup)
     t0 = time.perf_counter()
     ms_events = _events_ms(step, steps)
     torch.cuda.synchronize()
@@ -113,7 +137,7 @@ def bench_ssm(cfg, steps, warmup, level, shard=1):
         for _ in range(3):
             fwd()
             bwd()
-        n_k = max(steps, 10)
+        n_k = max(steps, 100)
         fwd_ms = _events_ms(fwd, n_k)
         bwd_ms = _events_ms(bwd, n_k)
 
@@ -149,6 +173,7 @@ def bench_ssm(cfg, steps, warmup, level, shard=1):
         "step_hbm": {"algorithmic_bytes": bytes_fwd + bytes_bwd, "achieved_GBps": gbs_step,
                      "frac_of_peak": gbs_step / HBM_PEAK_GBS},
         "wall_ms_per_step": wall_ms,
+        "warmup_steps_run": warm_run,
         "retained_after_forward_GB": kept / 1e9,
     }
     if shard > 1:  # what the shards would exchange: one all-reduce of the dB/dC partials (fp32)
@@ -195,9 +220,7 @@ def bench_transforms(cfg, steps, warmup):
            "unit": "elements/s", "dtype": "f32", "storage_dtype": "f16" if c["dtype"] == torch.float16 else "f32",
            "config": {"workload": f"{cfg} + fused transforms, B={B} L={L} D={D} N=16", "B": B, "L": L, "D": D}}
     for name, fn in (("fused", fused), ("unfused_torch_elementwise", unfused)):
-        for _ in range(warmup):
-            fn()
-        torch.cuda.synchronize()
+        _warmup(fn, warmup)
         ms = _events_ms(fn, steps)
         res[name] = {"ms_per_step": ms, "elements_per_s": B * L * D / (ms * 1e-3)}
     res["value"] = res["fused"]["elements_per_s"]
@@ -225,9 +248,7 @@ def bench_decode(cfg, steps, warmup, batch=None):
         m.step(*args, h, out_state=h)
 
     with torch.no_grad():
-        for _ in range(warmup):
-            step()
-        torch.cuda.synchronize()
+        _warmup(step, warmup)
         ms_eager = _events_ms(step, max(steps, 100))
         # a decode loop as a serving engine runs it: 32 steps captured once in a HIP graph, replayed
         graph = torch.cuda.CUDAGraph()
@@ -252,9 +273,7 @@ def bench_pscan(steps, warmup):
     from mamba_windows_cuda import parallel_scan_fn, workloads
 
     a, b = workloads.pscan_inputs(device="cuda", gen_device="cuda")
-    for _ in range(warmup):
-        parallel_scan_fn(a, b)
-    torch.cuda.synchronize()
+    _warmup(lambda: parallel_scan_fn(a, b), warmup)
     ms = _events_ms(lambda: parallel_scan_fn(a, b), steps)
     nbytes = 3 * 4 * a.numel()
     gbs = nbytes / (ms * 1e-3) / 1e9
@@ -287,9 +306,7 @@ def bench_stream(steps, warmup):
                                             x["C"][:, sl], x["D"], h)
         return h
 
-    for _ in range(warmup):
-        run()
-    torch.cuda.synchronize()
+    _warmup(run, warmup)
     ms = _events_ms(run, steps)
     from mamba_windows_cuda.workloads import algorithmic_bytes
 
@@ -365,8 +382,8 @@ def kernels_only(cfg):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="cfg2", choices=["cfg2", "cfg3", "cfg4a", "cfg4b"])
     ap.add_argument("--level", type=int, default=0, choices=[0, 1])
     ap.add_argument("--skip-cpu", action="store_true")
