@@ -50,7 +50,8 @@ enum mwc_status {
     MWC_ERR_INVALID_ARGUMENT = 1, /* shape/pointer/dtype contract violated */
     MWC_ERR_UNSUPPORTED = 2,      /* valid request the build does not handle */
     MWC_ERR_WORKSPACE = 3,        /* workspace missing or too small */
-    MWC_ERR_HIP = 4               /* a HIP runtime call failed */
+    MWC_ERR_HIP = 4,              /* a HIP runtime call failed */
+    MWC_ERR_INCOMPLETE = 5        /* device work gave up a bounded wait; its results are NaN */
 };
 
 /* Library version (MWC_ABI_VERSION). */
@@ -125,7 +126,6 @@ int mwc_ssm_bwd(int dtype, const void* u, const void* delta, const void* A, cons
                 void* dC, void* dD, void* dh_prev, int64_t batch, int64_t seqlen, int64_t dim,
                 int64_t dstate, void* workspace, size_t workspace_bytes, void* stream);
 
-/* Workspace bytes needed by mwc_pscan_fwd / mwc_pscan_bwd for these sizes. */
 /*
  * The adjoint of mwc_ssm_fwd_ex (no reference counterpart, see there). With z, `out` is the ungated
  * forward output (mwc_ssm_fwd_ex's `out`) and dout the gradient of out_z; dz receives
@@ -153,6 +153,7 @@ int mwc_ssm_step(int dtype, const void* u, const void* delta, const void* A, con
                  const void* D_ssm, const void* h, const void* delta_bias, int delta_softplus, const void* z,
                  void* out, void* out_z, void* h_new, int64_t batch, int64_t dim, int64_t dstate, void* stream);
 
+/* Workspace bytes needed by mwc_pscan_fwd / mwc_pscan_bwd for these sizes. */
 size_t mwc_pscan_workspace_size(int64_t nseq, int64_t seqlen, int64_t ncols);
 
 /*
@@ -171,6 +172,15 @@ int mwc_pscan_fwd(int dtype, const void* A, const void* X, void* H, int64_t nseq
 int mwc_pscan_bwd(int dtype, const void* A, const void* H, const void* dH, void* dA, void* dX,
                   int64_t nseq, int64_t seqlen, int64_t ncols, void* workspace,
                   size_t workspace_bytes, void* stream);
+
+/*
+ * Outcome of the last mwc_pscan_fwd / mwc_pscan_bwd that used `workspace` with these sizes: waits
+ * for `stream`, then returns MWC_OK, or MWC_ERR_INCOMPLETE if a bounded look-back wait between
+ * tiles ran out (the affected outputs are then NaN, never a silently wrong value). No reference
+ * counterpart: the reference's PScan (pscan.py:16-136) runs elementwise torch ops with no waits.
+ */
+int mwc_pscan_status(const void* workspace, size_t workspace_bytes, int64_t nseq, int64_t seqlen,
+                     int64_t ncols, void* stream);
 
 #ifdef __cplusplus
 }

@@ -198,6 +198,7 @@ const char* mwc_status_string(int status) {
         case MWC_ERR_UNSUPPORTED: return "MWC_ERR_UNSUPPORTED";
         case MWC_ERR_WORKSPACE: return "MWC_ERR_WORKSPACE";
         case MWC_ERR_HIP: return "MWC_ERR_HIP";
+        case MWC_ERR_INCOMPLETE: return "MWC_ERR_INCOMPLETE";
         default: return "MWC_ERR_UNKNOWN";
     }
 }
@@ -343,6 +344,15 @@ size_t mwc_pscan_workspace_size(int64_t nseq, int64_t seqlen, int64_t ncols) {
     return mwc::pscan_workspace_bytes(nseq, seqlen, ncols);
 }
 
+// Bound of each look-back wait of the scan (polls). MWC_PSCAN_SPIN_LIMIT overrides it (tests force a
+// give-up with 0: every wait then fails at once and every kernel still exits normally).
+static unsigned pscan_spin_limit() {
+    const char* e = getenv("MWC_PSCAN_SPIN_LIMIT");
+    if (!e || !*e) return mwc::kPscanSpinLimit;
+    const long long v = atoll(e);
+    return v < 0 ? mwc::kPscanSpinLimit : (unsigned)(v > (long long)mwc::kPscanSpinLimit ? mwc::kPscanSpinLimit : v);
+}
+
 static int check_pscan(int dtype, int64_t nseq, int64_t seqlen, int64_t ncols) {
     if (dtype != MWC_DTYPE_F32 && dtype != MWC_DTYPE_F16 && dtype != MWC_DTYPE_BF16)
         return fail(MWC_ERR_INVALID_ARGUMENT, "dtype must be MWC_DTYPE_F32, MWC_DTYPE_F16 or MWC_DTYPE_BF16 (got %d)",
@@ -364,7 +374,7 @@ int mwc_pscan_fwd(int dtype, const void* A, const void* X, void* H, int64_t nseq
     const size_t need = mwc::pscan_workspace_bytes(nseq, seqlen, ncols);
     if (need && (workspace == nullptr || workspace_bytes < need))
         return fail(MWC_ERR_WORKSPACE, "scan workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
-    MWC_HIP_TRY(mwc::launch_pscan_fwd(dtype, A, X, H, nseq, seqlen, ncols, workspace,
+    MWC_HIP_TRY(mwc::launch_pscan_fwd(dtype, A, X, H, nseq, seqlen, ncols, workspace, pscan_spin_limit(),
                                       (hipStream_t)stream));
     return MWC_OK;
 }
@@ -378,8 +388,26 @@ int mwc_pscan_bwd(int dtype, const void* A, const void* H, const void* dH, void*
     const size_t need = mwc::pscan_workspace_bytes(nseq, seqlen, ncols);
     if (need && (workspace == nullptr || workspace_bytes < need))
         return fail(MWC_ERR_WORKSPACE, "scan workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
-    MWC_HIP_TRY(mwc::launch_pscan_bwd(dtype, A, H, dH, dA, dX, nseq, seqlen, ncols, workspace,
+    MWC_HIP_TRY(mwc::launch_pscan_bwd(dtype, A, H, dH, dA, dX, nseq, seqlen, ncols, workspace, pscan_spin_limit(),
                                       (hipStream_t)stream));
+    return MWC_OK;
+}
+
+int mwc_pscan_status(const void* workspace, size_t workspace_bytes, int64_t nseq, int64_t seqlen, int64_t ncols,
+                     void* stream) {
+    g_err[0] = 0;
+    if (nseq <= 0 || seqlen <= 0 || ncols <= 0) return MWC_OK;  // nothing was scanned
+    const size_t need = mwc::pscan_workspace_bytes(nseq, seqlen, ncols);
+    if (workspace == nullptr || workspace_bytes < need)
+        return fail(MWC_ERR_WORKSPACE, "scan workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+    unsigned err = 0;
+    hipStream_t st = (hipStream_t)stream;
+    MWC_HIP_TRY(hipMemcpyAsync(&err, (const char*)workspace + mwc::pscan_error_word_offset(nseq, seqlen, ncols),
+                               sizeof(err), hipMemcpyDeviceToHost, st));
+    MWC_HIP_TRY(hipStreamSynchronize(st));
+    if (err != 0)
+        return fail(MWC_ERR_INCOMPLETE,
+                    "a look-back wait of the parallel scan ran out of spins: the affected tiles' outputs are NaN");
     return MWC_OK;
 }
 

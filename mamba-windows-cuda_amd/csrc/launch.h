@@ -90,12 +90,16 @@ hipError_t launch_ssm_step(int dt, int ns, const void* u, const void* delta, con
                            const void* C, const void* Dv, const void* h_in, const ScanXf& xf, void* y, void* y_z,
                            void* h_out, int64_t batch, int64_t dim, hipStream_t st);
 
+// spin_limit bounds every look-back wait (polls); a wait that runs out sets the workspace's error
+// word and poisons the tile's outputs with NaN.
 hipError_t launch_pscan_fwd(int dt, const void* A, const void* X, void* H, int64_t nseq,
-                            int64_t seqlen, int64_t ncols, void* ws, hipStream_t st);
+                            int64_t seqlen, int64_t ncols, void* ws, unsigned spin_limit, hipStream_t st);
 hipError_t launch_pscan_bwd(int dt, const void* A, const void* H, const void* dH, void* dA,
                             void* dX, int64_t nseq, int64_t seqlen, int64_t ncols, void* ws,
-                            hipStream_t st);
+                            unsigned spin_limit, hipStream_t st);
 size_t pscan_workspace_bytes(int64_t nseq, int64_t seqlen, int64_t ncols);
+size_t pscan_error_word_offset(int64_t nseq, int64_t seqlen, int64_t ncols);  // byte offset in the workspace
+constexpr unsigned kPscanSpinLimit = 1u << 22;  // default bound of a look-back wait (polls of ~128 clocks)
 
 // Grid helper: map hardware block ids so that consecutive logical blocks run on
 // the same XCD (the dispatcher deals block i to XCD i % 8), which keeps blocks

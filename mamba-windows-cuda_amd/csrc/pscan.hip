@@ -15,7 +15,10 @@
 // a single relaxed agent-scope atomic carries both the flag and the value
 // (no cache-wide release/acquire fences). Tiles are taken from an atomic
 // ticket so every predecessor of a waiting tile is already resident, and each
-// spin is bounded so a lost update can never hang the device.
+// spin is bounded so a lost update can never hang the device. A wait that runs
+// out of spins sets the workspace's error word (read by mwc_pscan_status) and
+// gives the tile a NaN prefix, so its outputs, and every later tile's, are NaN
+// rather than a plausible wrong value.
 #include <algorithm>
 
 #include "common.h"
@@ -27,7 +30,6 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kTileSteps = 128;
-constexpr unsigned kSpinLimit = 1u << 22;
 constexpr uint32_t kStAgg = 1, kStInc = 2;
 
 int pick_cw(int64_t ncols) { return ncols <= 16 ? 16 : (ncols <= 32 ? 32 : 64); }
@@ -58,15 +60,16 @@ __device__ __forceinline__ void publish(uint64_t* p, uint64_t w) {
     __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Wait until *p carries a non-zero status; returns the word (0 if the bounded spin ran out).
-__device__ __forceinline__ uint64_t wait_word(const uint64_t* p, unsigned* err) {
-    for (unsigned it = 0; it < kSpinLimit; ++it) {
+// Wait until *p carries a non-zero status; returns the word. If `limit` polls pass without one, the
+// error word is set and an inclusive NaN is returned: the tile's prefix, and so its outputs, are NaN.
+__device__ __forceinline__ uint64_t wait_word(const uint64_t* p, unsigned* err, unsigned limit) {
+    for (unsigned it = 0; it < limit; ++it) {
         const uint64_t w = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if ((w >> 32) != 0) return w;
         __builtin_amdgcn_s_sleep(2);
     }
     atomicOr(err, 1u);
-    return 0;
+    return pack(kStInc, __builtin_nanf(""));
 }
 
 }  // namespace
@@ -82,7 +85,8 @@ __global__ void __launch_bounds__(kThreads) pscan_kernel(const T* __restrict__ A
                                                          const T* __restrict__ Hs, T* __restrict__ Out,
                                                          T* __restrict__ dAo, uint64_t* __restrict__ flags,
                                                          unsigned* __restrict__ ticket, unsigned* __restrict__ err,
-                                                         int L, int ncols, int ncolblk, int64_t nchains) {
+                                                         int L, int ncols, int ncolblk, int64_t nchains,
+                                                         unsigned spin_limit) {
     constexpr int R = kThreads / CW;     // thread rows per tile
     constexpr int RUN = kTileSteps / R;  // steps per thread
     __shared__ int s_tile;
@@ -146,12 +150,12 @@ __global__ void __launch_bounds__(kThreads) pscan_kernel(const T* __restrict__ A
             float acc_a = 1.f, acc_h = 0.f;  // map of the tiles between the predecessor and this one
             uint64_t* pf = f - (int64_t)CW * 2;
             for (int j = lt - 1; j >= 0; --j, pf -= (int64_t)CW * 2) {
-                const uint64_t w = wait_word(pf, err);
-                if ((w >> 32) == kStInc || w == 0) {
+                const uint64_t w = wait_word(pf, err, spin_limit);
+                if ((w >> 32) == kStInc) {
                     prefix = __builtin_fmaf(acc_a, unpack_v(w), acc_h);
                     break;
                 }
-                const uint64_t wa = wait_word(pf + 1, err);
+                const uint64_t wa = wait_word(pf + 1, err, spin_limit);
                 acc_h = __builtin_fmaf(acc_a, unpack_v(w), acc_h);
                 acc_a *= unpack_v(wa);
             }
@@ -182,9 +186,14 @@ size_t pscan_workspace_bytes(int64_t nseq, int64_t seqlen, int64_t ncols) {
     return ((g.flag_bytes + 255) & ~(size_t)255) + 256;  // flags, then ticket + error word
 }
 
+size_t pscan_error_word_offset(int64_t nseq, int64_t seqlen, int64_t ncols) {
+    const PscanGeom g = geom(nseq, seqlen, ncols);
+    return ((g.flag_bytes + 255) & ~(size_t)255) + sizeof(unsigned);  // after the ticket
+}
+
 template <typename T, bool REV>
 static hipError_t pscan_t(const void* A, const void* X, const void* Hs, void* Out, void* dAo, int64_t nseq,
-                          int64_t seqlen, int64_t ncols, void* ws, hipStream_t st) {
+                          int64_t seqlen, int64_t ncols, void* ws, unsigned spin_limit, hipStream_t st) {
     const PscanGeom g = geom(nseq, seqlen, ncols);
     uint64_t* flags = (uint64_t*)ws;
     const size_t fb = (g.flag_bytes + 255) & ~(size_t)255;
@@ -198,7 +207,7 @@ static hipError_t pscan_t(const void* A, const void* X, const void* Hs, void* Ou
     if (g.cw == CWV)                                                                                              \
         hipLaunchKernelGGL((pscan_kernel<T, CWV, REV>), dim3((unsigned)g.ntiles), dim3(kThreads), 0, st,          \
                            (const T*)A, (const T*)X, (const T*)Hs, (T*)Out, (T*)dAo, flags, ticket, err,           \
-                           (int)seqlen, (int)ncols, g.ncolblk, g.nchains);
+                           (int)seqlen, (int)ncols, g.ncolblk, g.nchains, spin_limit);
     MWC_PSCAN_CW(16)
     MWC_PSCAN_CW(32)
     MWC_PSCAN_CW(64)
@@ -207,13 +216,15 @@ static hipError_t pscan_t(const void* A, const void* X, const void* Hs, void* Ou
 }
 
 hipError_t launch_pscan_fwd(int dt, const void* A, const void* X, void* H, int64_t nseq, int64_t seqlen,
-                            int64_t ncols, void* ws, hipStream_t st) {
-    MWC_DISPATCH_DTYPE(dt, TT, return pscan_t<TT, false>(A, X, nullptr, H, nullptr, nseq, seqlen, ncols, ws, st));
+                            int64_t ncols, void* ws, unsigned spin_limit, hipStream_t st) {
+    MWC_DISPATCH_DTYPE(dt, TT,
+                       return pscan_t<TT, false>(A, X, nullptr, H, nullptr, nseq, seqlen, ncols, ws, spin_limit, st));
 }
 
 hipError_t launch_pscan_bwd(int dt, const void* A, const void* H, const void* dH, void* dA, void* dX,
-                            int64_t nseq, int64_t seqlen, int64_t ncols, void* ws, hipStream_t st) {
-    MWC_DISPATCH_DTYPE(dt, TT, return pscan_t<TT, true>(A, dH, H, dX, dA, nseq, seqlen, ncols, ws, st));
+                            int64_t nseq, int64_t seqlen, int64_t ncols, void* ws, unsigned spin_limit,
+                            hipStream_t st) {
+    MWC_DISPATCH_DTYPE(dt, TT, return pscan_t<TT, true>(A, dH, H, dX, dA, nseq, seqlen, ncols, ws, spin_limit, st));
 }
 
 }  // namespace mwc

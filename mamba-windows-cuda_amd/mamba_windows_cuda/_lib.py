@@ -51,6 +51,8 @@ _SIGNATURES = {
     "mwc_pscan_workspace_size": ([I64, I64, I64], SZ),
     "mwc_pscan_fwd": ([ctypes.c_int, P, P, P, I64, I64, I64, P, SZ, P], ctypes.c_int),
     "mwc_pscan_bwd": ([ctypes.c_int, P, P, P, P, P, I64, I64, I64, P, SZ, P], ctypes.c_int),
+    # workspace, bytes, nseq, seqlen, ncols, stream
+    "mwc_pscan_status": ([P, SZ, I64, I64, I64, P], ctypes.c_int),
 }
 
 EXPORTED = tuple(_SIGNATURES)

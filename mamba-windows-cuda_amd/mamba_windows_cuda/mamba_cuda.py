@@ -157,7 +157,8 @@ def selective_scan_ref(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, return_int
 
     Returns (out (B,L,D), h_last (B,D,N)) and, with return_intermediates, a
     dict of the (B,D,N,L) tensors 'h_states', 'dA', 'dBu' plus the transposed
-    inputs. Not used by the GPU path.
+    inputs and, beyond the reference's keys, 'A' (which the adjoint of delta
+    needs; see selective_scan_backward). Not used by the GPU path.
     """
     bsz, L, dm = u.shape
     n = A.shape[1]
@@ -177,5 +178,51 @@ def selective_scan_ref(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, return_int
     out = y.transpose(1, 2)
     if return_intermediates:
         return out, h, {"h_states": h_states, "dA": dA, "dBu": dBu, "u_t": u_t, "delta_t": d_t,
-                        "B_t": B_t, "C_t": C_t, "h_prev": h_prev}
+                        "B_t": B_t, "C_t": C_t, "h_prev": h_prev, "A": A}
     return out, h
+
+
+def selective_scan_backward(dout, dh_last, intermediates, D_ssm):
+    """Gradients of the selective scan from ``selective_scan_ref``'s intermediates: the reference
+    API (mamba_cuda.py:949-1041), same arguments and return order
+    ``(du, ddelta, dA, dB_ssm, dC_ssm, dD_ssm, dh_prev)``; plain PyTorch on the intermediates'
+    device, not used by the GPU path.
+
+    Deliberate difference: this returns the true adjoint (what autograd gives through
+    ``selective_scan_ref``). The reference's loop hands du, ddelta and dB the decayed adjoint
+    dA_t*g_t where they need g_t (mamba_cuda.py:1012-1025), drops the A*dA_t*h_{t-1} term of
+    ddelta, and returns the gradient with respect to the decay factors, sum dh*h_{t-1}
+    (1009, 1033), instead of the one with respect to A. Here, with g_t = dout_t*C_t + dA_{t+1}*g_{t+1}
+    (g_{L-1} also receives dh_last):
+      du = D*dout + delta*sum_n g*B          ddelta = sum_n g*(A*dA_t*h_{t-1} + u*B)
+      dA = sum_{b,t} delta*g*dA_t*h_{t-1}    dB = sum_d g*delta*u    dC = sum_d dout*h_t
+      dD = sum_{b,t} dout*u                  dh_prev = dA_0*g_0
+    ``intermediates`` must also hold 'A' (D, N), which ``selective_scan_ref`` adds; ``dh_last``
+    may be None (zeros)."""
+    h_states, dA_t, u_t, d_t = (intermediates[k] for k in ("h_states", "dA", "u_t", "delta_t"))
+    B_t, C_t, h_prev = intermediates["B_t"], intermediates["C_t"], intermediates["h_prev"]
+    if "A" not in intermediates:
+        raise RuntimeError("selective_scan_backward needs intermediates['A'] (selective_scan_ref adds it)")
+    A = intermediates["A"]
+    bsz, dm, n, L = h_states.shape
+    dout_t = dout.transpose(1, 2).to(h_states.dtype)      # (B, D, L)
+    g = (torch.zeros_like(h_prev) if dh_last is None else dh_last.to(h_states.dtype)).clone()
+    du_t = torch.empty_like(u_t)
+    dd_t = torch.empty_like(d_t)
+    dB_t = torch.empty_like(B_t)
+    dC_t = torch.empty_like(C_t)
+    dA_acc = torch.zeros_like(h_prev)                     # (B, D, N), summed over b at the end
+    for t in range(L - 1, -1, -1):
+        g = g + dout_t[:, :, t, None] * C_t[:, None, :, t]  # g_t
+        prev = h_states[..., t - 1] if t > 0 else h_prev
+        s = g * dA_t[..., t] * prev                          # g_t * dA_t * h_{t-1}
+        S1 = (g * B_t[:, None, :, t]).sum(-1)                # sum_n g*B
+        du_t[:, :, t] = D_ssm * dout_t[:, :, t] + d_t[:, :, t] * S1
+        dd_t[:, :, t] = (A * s).sum(-1) + u_t[:, :, t] * S1
+        dA_acc = dA_acc + d_t[:, :, t, None] * s
+        dB_t[:, :, t] = (g * (d_t[:, :, t] * u_t[:, :, t])[:, :, None]).sum(1)
+        dC_t[:, :, t] = (dout_t[:, :, t, None] * h_states[..., t]).sum(1)
+        g = g * dA_t[..., t]                                 # carried to t - 1
+    dD = (u_t * dout_t).sum(dim=(0, 2))
+    return (du_t.transpose(1, 2), dd_t.transpose(1, 2), dA_acc.sum(0), dB_t.transpose(1, 2),
+            dC_t.transpose(1, 2), dD, g)

@@ -308,6 +308,16 @@ def _check_scan(*ts):
         _require(t.device == ts[0].device, "parallel_scan_fn inputs must share a device")
 
 
+def _pscan_status(L_, ws, nbytes, nseq, L, nc, dev, what):
+    """Raise if a bounded look-back wait of the scan just enqueued gave up (its outputs are then NaN).
+    Waits for the stream; skipped while a graph is being captured, where waiting is not allowed."""
+    if torch.cuda.is_current_stream_capturing():
+        return
+    with _on_device(dev):
+        st = L_.mwc_pscan_status(ws.data_ptr(), nbytes, nseq, L, nc, _stream(dev))
+    _lib.check(st, what)
+
+
 def pscan_forward(A, X):
     _check_scan(A, X)
     A, X = A.contiguous(), X.contiguous()
@@ -322,6 +332,7 @@ def pscan_forward(A, X):
         st = L_.mwc_pscan_fwd(_dtype_code(X), a3.data_ptr(), x3.data_ptr(), h3.data_ptr(), nseq, L, nc,
                               ws.data_ptr(), nbytes, _stream(X.device))
     _lib.check(st, "mwc_pscan_fwd")
+    _pscan_status(L_, ws, nbytes, nseq, L, nc, X.device, "mwc_pscan_fwd")
     return H
 
 
@@ -339,4 +350,5 @@ def pscan_backward(A, H, dH):
         st = L_.mwc_pscan_bwd(_dtype_code(H), a3.data_ptr(), h3.data_ptr(), g3.data_ptr(), da3.data_ptr(),
                               dx3.data_ptr(), nseq, L, nc, ws.data_ptr(), nbytes, _stream(H.device))
     _lib.check(st, "mwc_pscan_bwd")
+    _pscan_status(L_, ws, nbytes, nseq, L, nc, H.device, "mwc_pscan_bwd")
     return dA, dX

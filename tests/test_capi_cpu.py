@@ -197,3 +197,43 @@ def test_reference_api_functions_on_cpu():
     A = torch.rand(2, 3, 11, 5)
     X = torch.randn(2, 3, 11, 5)
     np.testing.assert_allclose(parallel_scan_ref(A, X).numpy(), orc.pscan_fwd(A, X), rtol=1e-5, atol=1e-6)
+
+
+def test_selective_scan_backward_is_the_true_adjoint():
+    """selective_scan_backward (the reference's API, mamba_cuda.py:949-1041) on selective_scan_ref's
+    intermediates: all seven gradients equal the float64 oracle's adjoint and torch autograd through
+    selective_scan_ref (rather than the reference loop's decayed-adjoint formulas)."""
+    import numpy as np
+
+    from mamba_windows_cuda.mamba_cuda import selective_scan_backward, selective_scan_ref
+    from oracle import oracle as orc
+
+    g = torch.Generator().manual_seed(12)
+    B, L, D, N = 2, 13, 5, 16
+    u = torch.randn(B, L, D, generator=g, dtype=torch.float64)
+    delta = 0.05 + 0.5 * torch.rand(B, L, D, generator=g, dtype=torch.float64)
+    A = -torch.rand(D, N, generator=g, dtype=torch.float64)
+    Bs = torch.randn(B, L, N, generator=g, dtype=torch.float64)
+    Cs = torch.randn(B, L, N, generator=g, dtype=torch.float64)
+    Dv = torch.randn(D, generator=g, dtype=torch.float64)
+    hp = torch.randn(B, D, N, generator=g, dtype=torch.float64)
+    dout = torch.randn(B, L, D, generator=g, dtype=torch.float64)
+    dhl = torch.randn(B, D, N, generator=g, dtype=torch.float64)
+    out, hl, inter = selective_scan_ref(u, delta, A, Bs, Cs, Dv, hp, return_intermediates=True)
+    got = selective_scan_backward(dout, dhl, inter, Dv)
+    ref = orc.ssm_bwd(u, delta, A, Bs, Cs, Dv, dout, hp, dhl)
+    names = ("du", "ddelta", "dA", "dB", "dC", "dD", "dh_prev")
+    for name, t in zip(names, got):
+        np.testing.assert_allclose(t.numpy(), ref[name], rtol=1e-10, atol=1e-12, err_msg=name)
+    leaves = [x.clone().requires_grad_(True) for x in (u, delta, A, Bs, Cs, Dv, hp)]
+    o2, h2 = selective_scan_ref(*leaves)
+    torch.autograd.backward([o2, h2], [dout, dhl])
+    for name, t, leaf in zip(names, got, leaves):
+        torch.testing.assert_close(t, leaf.grad, rtol=1e-10, atol=1e-12, msg=name)
+    # dh_last=None means zeros
+    got0 = selective_scan_backward(dout, None, inter, Dv)
+    ref0 = orc.ssm_bwd(u, delta, A, Bs, Cs, Dv, dout, hp, None)
+    np.testing.assert_allclose(got0[6].numpy(), ref0["dh_prev"], rtol=1e-10, atol=1e-12)
+    inter.pop("A")
+    with pytest.raises(RuntimeError, match="intermediates"):
+        selective_scan_backward(dout, dhl, inter, Dv)

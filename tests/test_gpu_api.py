@@ -1,0 +1,144 @@
+"""GPU parity of the reference API surfaces beyond SelectiveScanCuda.forward_with_state: the V1/V2
+autograd Functions, forward(h_prev) returning out only, parallel_scan_fn's adjoint at the config-4b
+length, the scan's bounded-wait error path, and the reference's long fp16 stream."""
+import numpy as np
+import pytest
+import torch
+
+from mamba_windows_cuda import SelectiveScanCuda, parallel_scan_fn, workloads
+from mamba_windows_cuda.mamba_cuda import SelectiveScanFn, SelectiveScanFnV2
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: dict(rtol=1e-3, atol=1e-4), torch.float16: dict(rtol=1e-2, atol=1e-2)}
+GRADS = (("u", "du"), ("delta", "ddelta"), ("A", "dA"), ("B", "dB"), ("C", "dC"), ("D", "dD"))
+
+
+def _np(t):
+    return t.detach().cpu().double().numpy()
+
+
+@pytest.mark.parametrize("fn", [SelectiveScanFn, SelectiveScanFnV2], ids=["V1_recompute", "V2_save"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_v1_v2_functions(dev, fn, dtype):
+    """SelectiveScanFn (reference V1, mamba_cuda.py:1099-1133) and SelectiveScanFnV2 (V2, 1136-1169):
+    out and the six gradients against the float64 oracle, gradients in the input dtype."""
+    print(f"case {fn.__name__} dtype={dtype}", flush=True)
+    x = workloads.ssm_inputs(2, 300, 200, dtype=dtype, seed=31)
+    leaves = {k: x[k].to(dev).requires_grad_(True) for k in ("u", "delta", "A", "B", "C", "D")}
+    out = fn.apply(leaves["u"], leaves["delta"], leaves["A"], leaves["B"], leaves["C"], leaves["D"])
+    assert out.dtype == dtype and tuple(out.shape) == (2, 300, 200)
+    out.backward(x["dout"].to(dev))
+    torch.cuda.synchronize()
+    ro, _ = orc.ssm_fwd(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], None, clamp=True)
+    np.testing.assert_allclose(_np(out), ro, err_msg="out", **TOL[dtype])
+    r = orc.ssm_bwd(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["dout"], None, None, clamp=True)
+    for k, name in GRADS:
+        assert leaves[k].grad.dtype == dtype, name
+        np.testing.assert_allclose(_np(leaves[k].grad), r[name], err_msg=name, **TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_forward_with_h_prev_returns_out_only(dev, dtype):
+    """SelectiveScanCuda.forward(..., h_prev) returns out alone (reference mamba_cuda.py:1190-1194), and
+    its backward reaches h_prev: dh_prev and the six gradients against the oracle."""
+    print(f"case forward(h_prev) dtype={dtype}", flush=True)
+    x = workloads.ssm_inputs(3, 150, 96, dtype=dtype, h_prev=True, seed=32)
+    names = ("u", "delta", "A", "B", "C", "D", "h_prev")
+    leaves = {k: x[k].to(dev).requires_grad_(True) for k in names}
+    out = SelectiveScanCuda()(*(leaves[k] for k in names))
+    assert isinstance(out, torch.Tensor) and tuple(out.shape) == (3, 150, 96)
+    out.backward(x["dout"].to(dev))
+    torch.cuda.synchronize()
+    ro, _ = orc.ssm_fwd(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["h_prev"], clamp=True)
+    np.testing.assert_allclose(_np(out), ro, err_msg="out", **TOL[dtype])
+    r = orc.ssm_bwd(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["dout"], x["h_prev"], None, clamp=True)
+    for k, name in GRADS + (("h_prev", "dh_prev"),):
+        np.testing.assert_allclose(_np(leaves[k].grad), r[name], err_msg=name, **TOL[dtype])
+
+
+def test_pscan_adjoint_config4b_length(dev):
+    """parallel_scan_fn forward and adjoint over one full config-4b sequence, (1, 65536, 1024) fp32:
+    512 tiles chained by the look-back in each direction, against the float64 scan and its adjoint."""
+    a, b = workloads.pscan_inputs((1, 65536, 1024), seed=3)
+    dH = torch.randn(1, 65536, 1024, generator=torch.Generator().manual_seed(4))
+    ad = a.to(dev).requires_grad_(True)
+    bd = b.to(dev).requires_grad_(True)
+    H = parallel_scan_fn(ad, bd)
+    H.backward(dH.to(dev))
+    torch.cuda.synchronize()
+    ref = orc.pscan_fwd(a, b)
+    np.testing.assert_allclose(_np(H), ref, rtol=1e-3, atol=1e-4)
+    rdA, rdX = orc.pscan_bwd(a, torch.from_numpy(ref), dH)
+    np.testing.assert_allclose(_np(bd.grad), rdX, rtol=1e-3, atol=1e-4)
+    np.testing.assert_allclose(_np(ad.grad), rdA, rtol=1e-3, atol=1e-4)
+
+
+def test_pscan_wait_give_up_is_reported(dev, monkeypatch):
+    """A look-back wait that runs out of polls is an error, not a silently wrong H: with a limit of 0
+    every wait gives up at once (each kernel still runs to its end), the host reports
+    MWC_ERR_INCOMPLETE, and the tiles that waited hold NaN. The default limit gives status OK."""
+    a, b = workloads.pscan_inputs((2, 1000, 64), seed=5)
+    ad, bd = a.to(dev), b.to(dev)
+    H = parallel_scan_fn(ad, bd)  # default limit: completes, status checked inside
+    np.testing.assert_allclose(_np(H), orc.pscan_fwd(a, b), rtol=1e-3, atol=1e-4)
+    from mamba_windows_cuda import _lib, ops
+
+    monkeypatch.setenv("MWC_PSCAN_SPIN_LIMIT", "0")
+    with pytest.raises(RuntimeError, match="MWC_ERR_INCOMPLETE"):
+        parallel_scan_fn(ad, bd)
+    # the raw C ABI: same outcome, and the first tile (no predecessor) is exact while later ones are NaN
+    L_ = _lib.lib()
+    nbytes = L_.mwc_pscan_workspace_size(2, 1000, 64)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    Hc = torch.empty_like(bd)
+    st = L_.mwc_pscan_fwd(_lib.MWC_DTYPE_F32, ad.data_ptr(), bd.data_ptr(), Hc.data_ptr(), 2, 1000, 64,
+                          ws.data_ptr(), nbytes, ops._stream(ad.device))
+    assert st == 0
+    assert L_.mwc_pscan_status(ws.data_ptr(), nbytes, 2, 1000, 64, ops._stream(ad.device)) == 5
+    Hc = Hc.cpu()
+    assert torch.isnan(Hc[:, 128:]).all()
+    torch.testing.assert_close(Hc[:, :128], H[:, :128].cpu(), rtol=0, atol=0)
+    monkeypatch.delenv("MWC_PSCAN_SPIN_LIMIT")
+    Hd = parallel_scan_fn(ad, bd)  # the next call with the default limit clears the word and completes
+    # (not bitwise: a tile's prefix sums its predecessors' aggregates or takes an inclusive prefix,
+    # whichever is published when it looks, so the rounding order varies from run to run)
+    torch.testing.assert_close(Hd, H, rtol=1e-5, atol=1e-5)
+
+
+def test_long_fp16_stream(dev):
+    """The reference's long-stream case (tests/test_selective_scan.py:218-237): 1280^2 fp16 steps fed in
+    16384-step chunks through forward_with_state at D=2048, so h_last is rounded to fp16 at ~100
+    chunk boundaries. Outputs and state stay finite, the streamed h equals one full-length pass, and
+    the float64 oracle over the whole sequence agrees on a 16-channel slice (u ~ 0.1 N(0,1),
+    delta = 0.01, A = -0.1 U(0,1), B, C ~ 0.1 N(0,1), D = 0.1, as the reference test draws them)."""
+    Bsz, D, N = 1, 2048, 16
+    L_total, chunk = 1280 * 1280, 16384
+    g = torch.Generator(device=dev).manual_seed(11)
+    u = (0.1 * torch.randn(Bsz, L_total, D, generator=g, device=dev)).half()
+    delta = torch.full((Bsz, L_total, D), 0.01, device=dev).half()
+    A = (-0.1 * torch.rand(D, N, generator=g, device=dev)).half()
+    Bs = (0.1 * torch.randn(Bsz, L_total, N, generator=g, device=dev)).half()
+    Cs = (0.1 * torch.randn(Bsz, L_total, N, generator=g, device=dev)).half()
+    Dv = torch.full((D,), 0.1, device=dev).half()
+    m = SelectiveScanCuda()
+    h = torch.zeros(Bsz, D, N, device=dev).half()
+    nchunks = (L_total + chunk - 1) // chunk
+    print(f"case long fp16 stream: {nchunks} chunks", flush=True)
+    with torch.no_grad():
+        for s in range(nchunks):
+            sl = slice(s * chunk, min(L_total, (s + 1) * chunk))
+            out, h = m.forward_with_state(u[:, sl], delta[:, sl], A, Bs[:, sl], Cs[:, sl], Dv, h)
+            if s == nchunks - 1:
+                last_out = out
+        _, h_full = m.forward_with_state(u, delta, A, Bs, Cs, Dv, None)
+    torch.cuda.synchronize()
+    assert torch.isfinite(last_out).all() and torch.isfinite(h).all()
+    torch.testing.assert_close(h, h_full, **TOL[torch.float16])
+    k = 16
+    ro, rh = orc.ssm_fwd(u[:, :, :k].cpu(), delta[:, :, :k].cpu(), A[:k].cpu(), Bs.cpu(), Cs.cpu(), Dv[:k].cpu(),
+                         None, clamp=True)
+    np.testing.assert_allclose(_np(h[:, :k]), rh, **TOL[torch.float16])
+    np.testing.assert_allclose(_np(h_full[:, :k]), rh, **TOL[torch.float16])
+    np.testing.assert_allclose(_np(last_out[:, :, :k]), ro[:, -last_out.shape[1]:], **TOL[torch.float16])
