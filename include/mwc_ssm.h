@@ -105,6 +105,21 @@ int mwc_ssm_fwd_ex(int dtype, const void* u, const void* delta, const void* A, c
                    int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate, void* workspace,
                    size_t workspace_bytes, void* stream);
 
+/*
+ * mwc_ssm_fwd_ex without a workspace argument: it allocates nothing and takes no workspace, for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation). No counterpart in the reference. The segment carries that
+ * mwc_ssm_fwd_ex keeps in its workspace live in a static device array of MWC_NOALLOC_SCRATCH_BYTES
+ * per GPU (held until the process ends); sizes whose carries need more (mwc_ssm_fwd_workspace_size)
+ * return MWC_ERR_UNSUPPORTED before anything is enqueued. Calls that overlap on one GPU share that
+ * array and race: serialise them (one stream, or events). Results equal mwc_ssm_fwd_ex's bitwise.
+ */
+#define MWC_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int mwc_ssm_fwd_noalloc(int dtype, const void* u, const void* delta, const void* A, const void* B_ssm,
+                        const void* C_ssm, const void* D_ssm, const void* h_prev, const void* delta_bias,
+                        int delta_softplus, const void* z, void* out, void* out_z, void* h_last, float* ckpt,
+                        int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate, void* stream);
+
 /* Workspace bytes needed by mwc_ssm_bwd for these sizes. */
 size_t mwc_ssm_bwd_workspace_size(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate);
 

@@ -8,6 +8,9 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "common.h"
 #include "launch.h"
 
@@ -187,6 +190,38 @@ size_t bwd_workspace_bytes(const SsmShape& s) {
 
 }  // namespace mwc
 
+// Scratch of mwc_ssm_fwd_noalloc: the forward's segment carries (h_end and the summed decay exponents
+// of every carry segment, fp32), for callers that cannot allocate. Each GPU the library runs on holds
+// its own copy until the process ends. The carry pass writes every value the main pass reads, so
+// nothing needs clearing; calls that overlap on one GPU share it and race.
+namespace {
+constexpr size_t kScratchBytes = MWC_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+std::mutex g_scratch_mu;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+
+// The current device's address of `scratch` (the symbol's name is only a host-side stand-in), looked
+// up once per device with that device current and kept for later calls.
+int device_scratch(void** out) {
+    int dev = -1;
+    MWC_HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return fail(MWC_ERR_UNSUPPORTED, "device index %d beyond %d", dev, kMaxDevices);
+    void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+        if (p == nullptr) {
+            MWC_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+            if (p == nullptr) return fail(MWC_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+            g_scratch_ptr[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return MWC_OK;
+}
+}  // namespace
+
 extern "C" {
 
 int mwc_abi_version(void) { return MWC_ABI_VERSION; }
@@ -217,11 +252,45 @@ size_t mwc_ssm_bwd_workspace_size(int64_t batch, int64_t seqlen, int64_t dim, in
     return mwc::bwd_workspace_bytes({batch, seqlen, dim, (int)dstate});
 }
 
+// The forward's one body: validation, workspace check and launch. With `scratch_only`, the segment
+// carries live in this device's static scratch array (mwc_ssm_fwd_noalloc) instead of a caller
+// workspace; sizes whose carries exceed it are rejected before anything is enqueued.
+static int fwd_impl(int dtype, const void* u, const void* delta, const void* A, const void* B_ssm,
+                    const void* C_ssm, const void* D_ssm, const void* h_prev, const void* delta_bias,
+                    int delta_softplus, const void* z, void* out, void* out_z, void* h_last, float* ckpt,
+                    int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate, void* workspace,
+                    size_t workspace_bytes, bool scratch_only, void* stream);
+
 int mwc_ssm_fwd_ex(int dtype, const void* u, const void* delta, const void* A, const void* B_ssm,
                    const void* C_ssm, const void* D_ssm, const void* h_prev, const void* delta_bias,
                    int delta_softplus, const void* z, void* out, void* out_z, void* h_last, float* ckpt,
                    int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate, void* workspace,
                    size_t workspace_bytes, void* stream) {
+    return fwd_impl(dtype, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, delta_bias, delta_softplus, z, out, out_z,
+                    h_last, ckpt, batch, seqlen, dim, dstate, workspace, workspace_bytes, false, stream);
+}
+
+int mwc_ssm_fwd_noalloc(int dtype, const void* u, const void* delta, const void* A, const void* B_ssm,
+                        const void* C_ssm, const void* D_ssm, const void* h_prev, const void* delta_bias,
+                        int delta_softplus, const void* z, void* out, void* out_z, void* h_last, float* ckpt,
+                        int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate, void* stream) {
+    return fwd_impl(dtype, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, delta_bias, delta_softplus, z, out, out_z,
+                    h_last, ckpt, batch, seqlen, dim, dstate, nullptr, 0, true, stream);
+}
+
+int mwc_ssm_fwd(int dtype, const void* u, const void* delta, const void* A, const void* B_ssm, const void* C_ssm,
+                const void* D_ssm, const void* h_prev, void* out, void* h_last, float* ckpt, int64_t batch,
+                int64_t seqlen, int64_t dim, int64_t dstate, void* workspace, size_t workspace_bytes,
+                void* stream) {
+    return mwc_ssm_fwd_ex(dtype, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, nullptr, 0, nullptr, out, nullptr,
+                          h_last, ckpt, batch, seqlen, dim, dstate, workspace, workspace_bytes, stream);
+}
+
+static int fwd_impl(int dtype, const void* u, const void* delta, const void* A, const void* B_ssm,
+                    const void* C_ssm, const void* D_ssm, const void* h_prev, const void* delta_bias,
+                    int delta_softplus, const void* z, void* out, void* out_z, void* h_last, float* ckpt,
+                    int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate, void* workspace,
+                    size_t workspace_bytes, bool scratch_only, void* stream) {
     g_err[0] = 0;
     if (int st = check_dims(dtype, batch, seqlen, dim, dstate)) return st;
     if (batch == 0 || dim == 0) return MWC_OK;
@@ -231,8 +300,17 @@ int mwc_ssm_fwd_ex(int dtype, const void* u, const void* delta, const void* A, c
     if (z == nullptr && out_z != nullptr) return fail(MWC_ERR_INVALID_ARGUMENT, "out_z needs z");
     const mwc::SsmShape s{batch, seqlen, dim, (int)dstate};
     hipStream_t st = (hipStream_t)stream;
-    const size_t need = mwc::fwd_workspace_bytes(s);
-    if (seqlen > 0 && need > 0 && (workspace == nullptr || workspace_bytes < need))
+    const size_t need = seqlen > 0 ? mwc::fwd_workspace_bytes(s) : 0;
+    if (scratch_only && need > 0) {
+        if (need > kScratchBytes)
+            return fail(MWC_ERR_UNSUPPORTED,
+                        "mwc_ssm_fwd_noalloc: these sizes need %zu bytes of segment carries, more than its static "
+                        "scratch of %zu bytes; call mwc_ssm_fwd_ex with a workspace instead",
+                        need, (size_t)kScratchBytes);
+        if (int e = device_scratch(&workspace)) return e;
+        workspace_bytes = kScratchBytes;
+    }
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need))
         return fail(MWC_ERR_WORKSPACE, "forward workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
     const mwc::SegPlan p = mwc::plan_fwd(s);
     float* car_h = (float*)workspace;
@@ -241,14 +319,6 @@ int mwc_ssm_fwd_ex(int dtype, const void* u, const void* delta, const void* A, c
                          p.nseg, p.cps, p.cfold, p.ncar, mwc::ScanXf{delta_bias, z, delta_softplus != 0}, out_z};
     MWC_HIP_TRY(mwc::launch_ssm_fwd(dtype, s.nstate, p.spl, a, s, st));
     return MWC_OK;
-}
-
-int mwc_ssm_fwd(int dtype, const void* u, const void* delta, const void* A, const void* B_ssm, const void* C_ssm,
-                const void* D_ssm, const void* h_prev, void* out, void* h_last, float* ckpt, int64_t batch,
-                int64_t seqlen, int64_t dim, int64_t dstate, void* workspace, size_t workspace_bytes,
-                void* stream) {
-    return mwc_ssm_fwd_ex(dtype, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, nullptr, 0, nullptr, out, nullptr,
-                          h_last, ckpt, batch, seqlen, dim, dstate, workspace, workspace_bytes, stream);
 }
 
 int mwc_ssm_bwd_ex(int dtype, const void* u, const void* delta, const void* A, const void* B_ssm,

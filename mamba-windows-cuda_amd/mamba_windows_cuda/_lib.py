@@ -20,6 +20,7 @@ MWC_DTYPE_F16 = 1
 MWC_DTYPE_BF16 = 2
 MWC_OK = 0
 CKPT_STEPS = 16  # MWC_CKPT_STEPS
+NOALLOC_SCRATCH_BYTES = 32 << 20  # MWC_NOALLOC_SCRATCH_BYTES
 
 _lock = threading.Lock()
 _lib = None
@@ -38,6 +39,9 @@ _SIGNATURES = {
     # dtype, u, delta, A, B, C, D, h_prev, delta_bias, softplus, z, out, out_z, h_last, ckpt, sizes, ws
     "mwc_ssm_fwd_ex": ([ctypes.c_int, P, P, P, P, P, P, P, P, ctypes.c_int, P, P, P, P, P, I64, I64, I64, I64,
                         P, SZ, P], ctypes.c_int),
+    # mwc_ssm_fwd_ex without the workspace arguments (static per-device scratch; allocates nothing)
+    "mwc_ssm_fwd_noalloc": ([ctypes.c_int, P, P, P, P, P, P, P, P, ctypes.c_int, P, P, P, P, P, I64, I64, I64,
+                             I64, P], ctypes.c_int),
     "mwc_ssm_bwd_workspace_size": ([I64, I64, I64, I64], SZ),
     "mwc_ssm_bwd": ([ctypes.c_int, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, P, SZ, P],
                     ctypes.c_int),

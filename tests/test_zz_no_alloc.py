@@ -1,0 +1,69 @@
+"""mwc_ssm_fwd_noalloc (the forward that allocates nothing, its segment carries in a static
+per-device scratch array) against mwc_ssm_fwd_ex with a caller workspace, through the C ABI:
+bitwise-equal outputs on two calls in a row, the second smaller, with L split into segments so that
+the scratch is used; and the size limit."""
+import ctypes
+
+import pytest
+import torch
+
+from mamba_windows_cuda import _lib, ops, workloads
+
+
+def _fwd_both(dev, B, L, D, dtype, *, xf, seed):
+    x = {k: v.to(dev) for k, v in workloads.ssm_inputs(B, L, D, dtype=dtype, h_prev=True, dout=False,
+                                                       seed=seed).items()}
+    bias = (0.3 * torch.randn(D, generator=torch.Generator().manual_seed(seed))).to(dtype).to(dev) if xf else None
+    z = torch.randn(B, L, D, generator=torch.Generator().manual_seed(seed + 1)).to(dtype).to(dev) if xf else None
+    L_ = _lib.lib()
+    nbytes = L_.mwc_ssm_fwd_workspace_size(B, L, D, 16)
+    assert 0 < nbytes <= _lib.NOALLOC_SCRATCH_BYTES  # L is split: the scratch is in use
+    nck = L_.mwc_ssm_ckpt_count(L)
+    results = []
+    for which in ("ex", "noalloc"):
+        out = torch.full_like(x["u"], float("nan"))
+        out_z = torch.full_like(x["u"], float("nan")) if xf else None
+        h_last = torch.full((B, D, 16), float("nan"), dtype=dtype, device=dev)
+        ckpt = torch.full((B, nck, D, 16), float("nan"), dtype=torch.float32, device=dev)
+        args = (ops._dtype_code(x["u"]), x["u"].data_ptr(), x["delta"].data_ptr(), x["A"].data_ptr(),
+                x["B"].data_ptr(), x["C"].data_ptr(), x["D"].data_ptr(), x["h_prev"].data_ptr(),
+                ops._ptr(bias), int(xf), ops._ptr(z), out.data_ptr(), ops._ptr(out_z), h_last.data_ptr(),
+                ckpt.data_ptr(), B, L, D, 16)
+        if which == "ex":
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+            st = L_.mwc_ssm_fwd_ex(*args, ws.data_ptr(), nbytes, ops._stream(x["u"].device))
+        else:
+            st = L_.mwc_ssm_fwd_noalloc(*args, ops._stream(x["u"].device))
+        _lib.check(st, which)
+        torch.cuda.synchronize()
+        results.append((out, out_z, h_last, ckpt))
+    return results
+
+
+@pytest.mark.gpu
+def test_noalloc_forward_matches_workspace_forward(dev, monkeypatch):
+    monkeypatch.setenv("MWC_NSEG", "3")
+    monkeypatch.setenv("MWC_CFOLD", "2")
+    # two calls in a row on the same GPU (the second smaller, with the fused transforms), each
+    # bitwise equal to the workspace entry point's results
+    for B, L, D, dtype, xf, seed in ((3, 700, 500, torch.float16, False, 61), (2, 300, 130, torch.float32, True, 62)):
+        print(f"case noalloc B={B} L={L} D={D} dtype={dtype} transforms={xf}", flush=True)
+        (o1, z1, h1, c1), (o2, z2, h2, c2) = _fwd_both(dev, B, L, D, dtype, xf=xf, seed=seed)
+        assert torch.isfinite(o1).all() and torch.isfinite(h1).all() and torch.isfinite(c1).all()
+        assert torch.equal(o1, o2) and torch.equal(h1, h2) and torch.equal(c1, c2)
+        if xf:
+            assert torch.isfinite(z1).all() and torch.equal(z1, z2)
+
+
+def test_noalloc_forward_rejects_sizes_beyond_its_scratch(monkeypatch):
+    """Carries beyond MWC_NOALLOC_SCRATCH_BYTES: MWC_ERR_UNSUPPORTED before anything is enqueued (the
+    pointers are never dereferenced, so this runs without a GPU)."""
+    monkeypatch.setenv("MWC_NSEG", "16")
+    monkeypatch.setenv("MWC_CFOLD", "4")
+    L_ = _lib.lib()
+    B, L, D = 64, 8192, 8192
+    assert L_.mwc_ssm_fwd_workspace_size(B, L, D, 16) > _lib.NOALLOC_SCRATCH_BYTES
+    fake = ctypes.c_void_p(256)
+    st = L_.mwc_ssm_fwd_noalloc(1, fake, fake, fake, fake, fake, fake, None, None, 0, None, fake, None, None, None,
+                                B, L, D, 16, None)
+    assert st == 2 and b"scratch" in L_.mwc_last_error()
