@@ -280,6 +280,135 @@ template <int G, int V> __device__ __forceinline__ float reduce_scatter(float (&
     return reduce_scatter_lv<G, V>(x, lane);
 }
 
+// Reduce-scatter over the LPC = 64/CPW lanes of a channel when the wave's CPW channels occupy the
+// low lane bits (channel = lane % CPW, state group = lane / CPW): the partners of a channel's lanes
+// differ in lane bits log2(CPW)..5, and every such bit has a two-instruction exchange on gfx950 --
+// bits 4 and 5 swap rows / halves of a register pair (v_permlane16_swap_b32, v_permlane32_swap_b32),
+// bits 3 and 2 are DPP reads of lane +-8 / +-4 whose halves are selected by bank masks. So each level
+// costs two instructions per value it leaves (no selects), and a last single-value level on a DPP bit
+// costs one. Level order: the permlane bits first (while two or more values remain), then bits 3, 2.
+// At a level on lane bit b the lanes with bit b = 0 keep the even values (2q) and the others the odd
+// ones (2q+1), each adding its partner's copy; the lane returns the group sum of value
+// rs_hi_index<CPW, V>(lane). The clang builtins for the permlane swaps drop their second result in this
+// toolchain, so they are written as inline assembly with both registers read and written; a leading
+// s_nop covers the read-after-VALU-write wait states of DPP and permlane sources.
+template <int CPW> constexpr int hi_log() { return CPW >= 16 ? 4 : CPW >= 8 ? 3 : CPW >= 4 ? 2 : CPW >= 2 ? 1 : 0; }
+template <int CPW> constexpr int hi_bit(int level) {
+    constexpr int order[6] = {4, 5, 3, 2, 1, 0};
+    int k = 0;
+    for (int i = 0; i < 6; ++i)
+        if (order[i] >= hi_log<CPW>()) {
+            if (k == level) return order[i];
+            ++k;
+        }
+    return -1;
+}
+template <int CPW, int V> __device__ __forceinline__ int rs_hi_index(int lane) {
+    int idx = 0;
+#pragma unroll
+    for (int l = 0; (1 << l) < V; ++l) idx |= ((lane >> hi_bit<CPW>(l)) & 1) << l;
+    return idx;
+}
+
+// v_permlane{16,32}_swap_b32 on NP register pairs (x[2q], x[2q+1]), in place
+template <int BIT, int NP> __device__ __forceinline__ void permlane_swap_pairs(float* x);
+#define MWC_PL(BIT, INS)                                                                                       \
+    template <> __device__ __forceinline__ void permlane_swap_pairs<BIT, 1>(float* x) {                        \
+        asm("s_nop 1\n\t" INS " %0, %1" : "+v"(x[0]), "+v"(x[1]));                                              \
+    }                                                                                                          \
+    template <> __device__ __forceinline__ void permlane_swap_pairs<BIT, 2>(float* x) {                        \
+        asm("s_nop 1\n\t" INS " %0, %1\n\t" INS " %2, %3" : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]));  \
+    }                                                                                                          \
+    template <> __device__ __forceinline__ void permlane_swap_pairs<BIT, 4>(float* x) {                        \
+        asm("s_nop 1\n\t" INS " %0, %1\n\t" INS " %2, %3\n\t" INS " %4, %5\n\t" INS " %6, %7"                  \
+            : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]), "+v"(x[6]), "+v"(x[7])); \
+    }                                                                                                          \
+    template <> __device__ __forceinline__ void permlane_swap_pairs<BIT, 8>(float* x) {                        \
+        permlane_swap_pairs<BIT, 4>(x);                                                                        \
+        permlane_swap_pairs<BIT, 4>(x + 8);                                                                    \
+    }
+MWC_PL(4, "v_permlane16_swap_b32")
+MWC_PL(5, "v_permlane32_swap_b32")
+#undef MWC_PL
+
+// DPP levels on lane bit 3 (partner lane ^ 8: row_ror:8; banks 0,1 keep half 0) and bit 2 (partner
+// lane + 4 on banks 0,2 via row_shl:4, lane - 4 on banks 1,3 via row_shr:4; banks 0,2 keep half 0)
+#define MWC_HADD(o, i0, i1, c0, c1, m0, m1)                                                          \
+    "v_add_f32_dpp %" #o ", %" #i0 ", %" #i0 " " c0 " row_mask:0xf bank_mask:" m0 "\n\t"              \
+    "v_add_f32_dpp %" #o ", %" #i1 ", %" #i1 " " c1 " row_mask:0xf bank_mask:" m1 "\n\t"
+template <int BIT, int NP> __device__ __forceinline__ void dpp_hi_level(const float* x, float* r);
+#define MWC_HLEVEL(BIT, C0, C1, M0, M1)                                                                    \
+    template <> __device__ __forceinline__ void dpp_hi_level<BIT, 1>(const float* x, float* r) {          \
+        asm("s_nop 1\n\t" MWC_HADD(0, 1, 2, C0, C1, M0, M1) : "=&v"(r[0]) : "v"(x[0]), "v"(x[1]));         \
+    }                                                                                                      \
+    template <> __device__ __forceinline__ void dpp_hi_level<BIT, 2>(const float* x, float* r) {          \
+        asm("s_nop 1\n\t" MWC_HADD(0, 2, 3, C0, C1, M0, M1) MWC_HADD(1, 4, 5, C0, C1, M0, M1)              \
+            : "=&v"(r[0]), "=&v"(r[1])                                                                     \
+            : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]));                                                 \
+    }                                                                                                      \
+    template <> __device__ __forceinline__ void dpp_hi_level<BIT, 4>(const float* x, float* r) {          \
+        asm("s_nop 1\n\t" MWC_HADD(0, 4, 5, C0, C1, M0, M1) MWC_HADD(1, 6, 7, C0, C1, M0, M1)              \
+                MWC_HADD(2, 8, 9, C0, C1, M0, M1) MWC_HADD(3, 10, 11, C0, C1, M0, M1)                      \
+            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])                                           \
+            : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]), "v"(x[5]), "v"(x[6]), "v"(x[7]));     \
+    }                                                                                                      \
+    template <> __device__ __forceinline__ void dpp_hi_level<BIT, 8>(const float* x, float* r) {          \
+        dpp_hi_level<BIT, 4>(x, r);                                                                        \
+        dpp_hi_level<BIT, 4>(x + 8, r + 4);                                                                \
+    }
+MWC_HLEVEL(3, "row_ror:8", "row_ror:8", "0x3", "0xc")
+MWC_HLEVEL(2, "row_shl:4", "row_shr:4", "0x5", "0xa")
+#undef MWC_HLEVEL
+#undef MWC_HADD
+
+// x + its partner's x at a single-value level
+template <int BIT> __device__ __forceinline__ float hi_single(float x) {
+    float r;
+    if constexpr (BIT == 3) {
+        asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %1 row_ror:8 row_mask:0xf bank_mask:0xf" : "=v"(r) : "v"(x));
+    } else if constexpr (BIT == 2) {
+        asm("s_nop 1\n\t"
+            "v_add_f32_dpp %0, %1, %1 row_shl:4 row_mask:0xf bank_mask:0x5\n\t"
+            "v_add_f32_dpp %0, %1, %1 row_shr:4 row_mask:0xf bank_mask:0xa"
+            : "=&v"(r)
+            : "v"(x));
+    } else {
+        float pair[2] = {x, x};
+        permlane_swap_pairs<BIT, 1>(pair);
+        r = pair[0] + pair[1];
+    }
+    return r;
+}
+
+template <int CPW, int V, int L = 0, int M = V>
+__device__ __forceinline__ float reduce_scatter_hi_lv(float (&x)[V]) {
+    constexpr int B = hi_bit<CPW>(L);
+    static_assert(B != 0 && B != 1, "lane bits 0 and 1 are not part of a channel's lane group here");
+    if constexpr (B < 0) {
+        return x[0];
+    } else if constexpr (M > 1) {
+        if constexpr (B >= 4) {
+            permlane_swap_pairs<B, M / 2>(x);
+#pragma unroll
+            for (int q = 0; q < M / 2; ++q) x[q] = x[2 * q] + x[2 * q + 1];
+        } else {
+            float r[M / 2];
+            dpp_hi_level<B, M / 2>(x, r);
+#pragma unroll
+            for (int q = 0; q < M / 2; ++q) x[q] = r[q];
+        }
+        return reduce_scatter_hi_lv<CPW, V, L + 1, M / 2>(x);
+    } else {
+        x[0] = hi_single<B>(x[0]);
+        return reduce_scatter_hi_lv<CPW, V, L + 1, 1>(x);
+    }
+}
+// x is clobbered; V (a power of two) values, 2 <= V <= 64/CPW.
+template <int CPW, int V> __device__ __forceinline__ float reduce_scatter_hi(float (&x)[V]) {
+    static_assert(V >= 2 && (V & (V - 1)) == 0 && V * CPW <= 64, "shape");
+    return reduce_scatter_hi_lv<CPW, V>(x);
+}
+
 }  // namespace mwc
 
 #define MWC_HIP_TRY(expr)                                  \

@@ -307,23 +307,32 @@ ssm_bwd_kernel(
     constexpr int OS = CPB + 4;
     constexpr int BCN = TC * NS;                       // B (and C) values per chunk
     constexpr int BCPT = BCN >= 256 ? BCN / 256 : 1;   // of them per loader thread
-    // fold: each 4-step phase produces 2*NS values (dB, dC) per slot, NQ groups of 4 per slot; the
-    // 16 lanes of a slot take NQ groups, LPI lanes per group splitting the channels (or, past 16
-    // groups, QPL groups per lane)
-    constexpr int NQ = NS / 2;
-    constexpr int LPI = NQ <= 16 ? 16 / NQ : 1;
-    constexpr int QPL = NQ <= 16 ? 1 : NQ / 16;
-    static_assert(NSG * SPG == TC && CPW >= LPI && (BCN < 256 || BCN % 256 == 0) && LPI <= 4, "tiling");
+    // fold: each 4-step phase produces, per slot (step), 2*NS sums over the wave's CPW channels (dB and
+    // dC); the 16 lanes of a slot take one (plane, block of VB = NS/8 states) each and sum all CPW
+    // channels themselves, so no lane pair has to combine partial sums
+    constexpr int VB = NS / 8;
+    static_assert(NSG * SPG == TC && (BCN < 256 || BCN % 256 == 0) && VB >= 1, "tiling");
 
     // [delta, delta*u, dout] planes of [channel][step]; planes are AS floats apart
     // (AS = 16 mod 64 banks) so the delta*u and dout weights of one channel sit in different banks
     constexpr int AS = CPB * RS + 16;
     __shared__ __align__(16) float s_in_raw[3 * AS];
+    // the fold's weights (delta*u for dB, dout for dC) transposed, [plane][step][channel], so a fold lane
+    // reads its slot's CPW weights as vectors; the planes are 32 banks apart (a slot's lanes read one
+    // row of each at once)
+    constexpr int WS = CPB + 4, WP = TC * WS + 32;
+    __shared__ __align__(16) float s_wt_raw[2 * WP];
+    auto s_wt = [&](int plane, int step) -> float* { return &s_wt_raw[plane * WP + step * WS]; };
     // B/C rows of the chunk, [step][n / SPL][B x SPL, C x SPL]: a lane reads its B and C with one access
     __shared__ __align__(16) float s_bc[TC][2 * NS];
-    // wave-private slabs of g_t (plane 0) and h_t (plane 1): [wave][plane][slot][channel][16];
-    // a 16-lane group deposits 64 consecutive floats, plane 1 is offset by 32 banks
-    constexpr int PL = kRedSlots * CPW * NS + 32;
+    // wave-private slabs of g_t (plane 0) and h_t (plane 1): [wave][plane][slot][state block][channel][VB],
+    // a (slot, block) row holding the VB states of the block for every channel of the wave, rows packed
+    // and plane 1 starting 4 floats past a multiple of 8. Measured on gfx950 (N=16, 8 lanes per channel):
+    // the deposits (ds_write_b64 by lane (channel, block) into row block, column channel) then run
+    // without bank conflicts, and so do the fold's ds_read_b128 of whole rows when the lanes of rows 4..7
+    // of a group take the row's four 16-byte pieces in the order 2, 3, 0, 1 (see the fold)
+    constexpr int RW = CPW * VB;
+    constexpr int PL = kRedSlots * 8 * RW + 4;
     __shared__ __align__(16) float s_red[4][2 * PL];
     auto s_in = [&](int plane, int ch) -> float* { return &s_in_raw[plane * AS + ch * RS]; };
     __shared__ __align__(16) float s_part[4][TC][2 * NS];
@@ -341,9 +350,11 @@ ssm_bwd_kernel(
     const int k1 = min(nck, k0 + cps);
 
     const int wave = tid >> 6, lane = tid & 63;
-    const int cw = lane / LPC;  // channel within the wave
+    // a wave's CPW channels take the low lane bits (channel lane % CPW, state group lane / CPW), so a
+    // channel's lanes differ in the high bits the reduce-scatter exchanges cheaply
+    const int cw = lane % CPW;  // channel within the wave
     const int c = wave * CPW + cw;
-    const int g = lane % LPC;
+    const int g = lane / CPW;
     const int n0 = g * SPL;
     const bool valid = d0 + c < D;
     const int d = valid ? d0 + c : D - 1;
@@ -353,9 +364,11 @@ ssm_bwd_kernel(
     const int ld_d = lvalid ? d0 + lc : D - 1;
     const int64_t row0 = (int64_t)b * L;
 
-    // folding roles: slot rs (step i+rs), first value group rq0 (groups < NQ/2 are dB n = 4*group..,
-    // the rest dC), channel subset rsub of the group's LPI lanes
-    const int rs = lane >> 4, rq0 = ((lane & 15) / LPI) * QPL, rsub = (lane & 15) % LPI;
+    // folding roles: slot rs (step i+rs), plane rpl (0: dB from g, 1: dC from h), state block rb; with
+    // rows of 8 channels x 2 states, lanes rb >= 4 read their row's halves in swapped order (frot)
+    const int rs = lane >> 4, rpl = (lane >> 3) & 1, rb = lane & 7;
+    constexpr bool kFoldRot = CPW == 8 && VB == 2;
+    const int frot = kFoldRot ? rb >> 2 : 0;
 
     float A2[SPL], An[SPL], gc[SPL], dAacc[SPL];
 #pragma unroll
@@ -484,6 +497,11 @@ ssm_bwd_kernel(
         stv<SPG>((s_in(1, lc) + sg * SPG), vdu);
         stv<SPG>((s_in(2, lc) + sg * SPG), vy);
 #pragma unroll
+        for (int s = 0; s < SPG; ++s) {  // the fold's weights, transposed
+            s_wt(0, sg * SPG + s)[lc] = vdu[s];
+            s_wt(1, sg * SPG + s)[lc] = vy[s];
+        }
+#pragma unroll
         for (int q = 0; q < BCPT; ++q) {
             const int e = tid * BCPT + q;
             if (BCN >= 256 || e < BCN) {
@@ -506,8 +524,8 @@ ssm_bwd_kernel(
     }
     __syncthreads();
 
-    float* red_g = &s_red[wave][0];   // [slot][channel][16]
-    float* red_h = &s_red[wave][PL];  // [slot][channel][16]
+    float* red_g = &s_red[wave][0];   // [slot][state block][channel][VB]
+    float* red_h = &s_red[wave][PL];
 
     ProgressPrio prio(k1 - k0);
     for (int k = k1 - 1; k >= k0; --k) {
@@ -564,46 +582,29 @@ ssm_bwd_kernel(
         // B/C are read one step ahead and delta/dout one 4-step group ahead of use; every 4 steps the
         // wave folds the phase's deposits over its channels.
         auto fold = [&](int phase) {
-#pragma unroll
-            for (int qq = 0; qq < QPL; ++qq) {
-                const int rq = rq0 + qq;
-                const bool is_c = rq >= NQ / 2;
-                const float* plane = is_c ? red_h : red_g;
-                const float* wrow = s_in(is_c ? 2 : 1, wave * CPW) + phase * kRedSlots + rs;
-                const int q4 = (rq % (NQ / 2)) * 4;
-                float acc[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int m = 0; m < CPW / LPI; ++m) {
-                    const int ch = LPI * m + rsub;  // the LPI lanes of a group take interleaved channels
-                    float v4[4];
-                    ldv<4>(plane + (rs * CPW + ch) * NS + q4, v4);
-                    const float wgt = wrow[ch * RS];
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) acc[q] = __builtin_fmaf(v4[q], wgt, acc[q]);
-                }
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    if constexpr (LPI >= 2) acc[q] += dpp<kDppXor1>(acc[q]);
-                    if constexpr (LPI >= 4) acc[q] += dpp<kDppXor2>(acc[q]);
-                }
-                float* const dst = &s_part[wave][phase * kRedSlots + rs][rq * 4];
-                if constexpr (LPI == 1) {
-                    stv<4>(dst, acc);
-                } else {
-                    // every lane of the group holds the 4 sums: each writes its 4/LPI of them (narrow
-                    // LDS writes cost less than one 16-byte write by one lane)
-                    constexpr int W = 4 / LPI;
-                    float w[W];
-#pragma unroll
-                    for (int q = 0; q < W; ++q) {
-                        if constexpr (LPI == 2)
-                            w[q] = rsub ? acc[2 + q] : acc[q];
-                        else
-                            w[q] = (rsub & 2) ? ((rsub & 1) ? acc[3] : acc[2]) : ((rsub & 1) ? acc[1] : acc[0]);
-                    }
-                    stv<W>(dst + rsub * W, w);
-                }
+            // this lane's (slot, plane, block) row: the block's VB states for each of the CPW channels
+            float v[CPW * VB], w[CPW], acc[VB];
+            const float* row = (rpl ? red_h : red_g) + (rs * 8 + rb) * RW;
+            const float* wrow = s_wt(rpl, phase * kRedSlots + rs) + wave * CPW;
+            if constexpr (kFoldRot) {
+                // rows of 16 floats (8 channels x 2 states): lanes rb >= 4 read the halves of the row, and
+                // of the weights, swapped; channel order does not matter to the sum
+                ldv<8>(row + 8 * frot, *reinterpret_cast<float(*)[8]>(v));
+                ldv<8>(row + 8 - 8 * frot, *reinterpret_cast<float(*)[8]>(v + 8));
+                ldv<4>(wrow + 4 * frot, *reinterpret_cast<float(*)[4]>(w));
+                ldv<4>(wrow + 4 - 4 * frot, *reinterpret_cast<float(*)[4]>(w + 4));
+            } else {
+                ldv<CPW * VB>(row, v);
+                ldv<CPW>(wrow, w);
             }
+#pragma unroll
+            for (int q = 0; q < VB; ++q) acc[q] = v[q] * w[0];
+#pragma unroll
+            for (int ch = 1; ch < CPW; ++ch) {
+#pragma unroll
+                for (int q = 0; q < VB; ++q) acc[q] = __builtin_fmaf(v[ch * VB + q], w[ch], acc[q]);
+            }
+            stv<VB>(&s_part[wave][phase * kRedSlots + rs][rpl * NS + rb * VB], acc);
         };
         {
             float yq[4], dq[4], yqn[4], dqn[4], Bn[SPL], Cn[SPL];
@@ -613,7 +614,7 @@ ssm_bwd_kernel(
             // The storing threads add u*S1 once per element.
             constexpr int RV = LPC, RST = RV / 2;
             float rp[RV];
-            const int ridx = rs_index<LPC, RV>(lane);
+            const int ridx = rs_hi_index<CPW, RV>(lane);
             float* const s_mine = &s_out[ridx & 1][ridx >> 1][c];  // + the round's first step * OS
             ldv<4>(s_in(2, c) + TC - 4, yqn);
             ldv<4>(s_in(0, c) + TC - 4, dqn);
@@ -668,10 +669,21 @@ ssm_bwd_kernel(
                 }
                 rp[2 * (i % RST)] = r1;
                 rp[2 * (i % RST) + 1] = r2;
-                if (i % RST == 0) s_mine[i * OS] = reduce_scatter<LPC, RV>(rp, lane);
-                const int sl = slot * CPW + cw;
-                stv<SPL>(red_g + sl * NS + n0, gt);
-                stv<SPL>(red_h + sl * NS + n0, H[i]);
+                if (i % RST == 0) s_mine[i * OS] = reduce_scatter_hi<CPW, RV>(rp);
+                // deposit g_t and h_t: state n goes to row (slot, n / VB), column cw * VB + n % VB
+                constexpr int DW = SPL < VB ? SPL : VB;  // floats per deposit write
+#pragma unroll
+                for (int j0 = 0; j0 < SPL; j0 += DW) {
+                    const int n = n0 + j0, o = (slot * 8 + n / VB) * RW + cw * VB + n % VB;
+                    float wg[DW], wh[DW];
+#pragma unroll
+                    for (int q = 0; q < DW; ++q) {
+                        wg[q] = gt[j0 + q];
+                        wh[q] = H[i][j0 + q];
+                    }
+                    stv<DW>(red_g + o, wg);
+                    stv<DW>(red_h + o, wh);
+                }
                 if (slot == 0) {
                     wave_lds_fence();
                     fold(phase);
