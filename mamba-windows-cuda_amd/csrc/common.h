@@ -380,6 +380,30 @@ template <int BIT> __device__ __forceinline__ float hi_single(float x) {
     return r;
 }
 
+// One reduce-scatter level on lane bit PB for NP value pairs (x[2q], x[2q+1]): lanes whose bit PB is 0
+// get x[2q] + the partner's x[2q], the others x[2q+1] + the partner's x[2q+1] (partner = lane ^ 2^PB).
+// Bits 2 and 3 are bank-masked DPP reads, 4 and 5 permlane swaps, 0 and 1 selects and a DPP add.
+template <int PB, int NP> __device__ __forceinline__ void pair_level(const float* x, float* r, int lane) {
+    if constexpr (PB == 2 || PB == 3) {
+        dpp_hi_level<PB, NP>(x, r);
+    } else if constexpr (PB == 4 || PB == 5) {
+        float t[2 * NP];
+#pragma unroll
+        for (int q = 0; q < 2 * NP; ++q) t[q] = x[q];
+        permlane_swap_pairs<PB, NP>(t);
+#pragma unroll
+        for (int q = 0; q < NP; ++q) r[q] = t[2 * q] + t[2 * q + 1];
+    } else {
+        const bool hi = ((lane >> PB) & 1) != 0;
+#pragma unroll
+        for (int q = 0; q < NP; ++q) {
+            const float keep = hi ? x[2 * q + 1] : x[2 * q];
+            const float send = hi ? x[2 * q] : x[2 * q + 1];
+            r[q] = keep + dpp_flip<PB>(send);
+        }
+    }
+}
+
 template <int CPW, int V, int L = 0, int M = V>
 __device__ __forceinline__ float reduce_scatter_hi_lv(float (&x)[V]) {
     constexpr int B = hi_bit<CPW>(L);

@@ -307,32 +307,31 @@ ssm_bwd_kernel(
     constexpr int OS = CPB + 4;
     constexpr int BCN = TC * NS;                       // B (and C) values per chunk
     constexpr int BCPT = BCN >= 256 ? BCN / 256 : 1;   // of them per loader thread
-    // fold: each 4-step phase produces, per slot (step), 2*NS sums over the wave's CPW channels (dB and
-    // dC); the 16 lanes of a slot take one (plane, block of VB = NS/8 states) each and sum all CPW
-    // channels themselves, so no lane pair has to combine partial sums
+    // dB/dC over the wave's channels: each step a lane weights g_t (by delta*u) and h_t (by dout) in
+    // registers and adds its channel partner's (the lane 2^PB away: channels c and c ^ CPW/2) with one
+    // reduce-scatter level, keeping the g sums on one side and the h sums on the other, and deposits
+    // that one vector. Every 4-step phase the 16 lanes of a slot each take one (plane, block of VB =
+    // NS/8 states) row and add its CPW/2 channel-pair columns, so no lane pair combines partial sums
+    // and the fold needs no weights.
     constexpr int VB = NS / 8;
+    constexpr int PB = CPW >= 16 ? 3 : CPW >= 8 ? 2 : 1;  // lane bit of the channel partner (top channel bit)
+    constexpr int NPC = CPW / 2;                           // channel-pair columns per row
     static_assert(NSG * SPG == TC && (BCN < 256 || BCN % 256 == 0) && VB >= 1, "tiling");
 
     // [delta, delta*u, dout] planes of [channel][step]; planes are AS floats apart
     // (AS = 16 mod 64 banks) so the delta*u and dout weights of one channel sit in different banks
     constexpr int AS = CPB * RS + 16;
     __shared__ __align__(16) float s_in_raw[3 * AS];
-    // the fold's weights (delta*u for dB, dout for dC) transposed, [plane][step][channel], so a fold lane
-    // reads its slot's CPW weights as vectors; the planes are 32 banks apart (a slot's lanes read one
-    // row of each at once)
-    constexpr int WS = CPB + 4, WP = TC * WS + 32;
-    __shared__ __align__(16) float s_wt_raw[2 * WP];
-    auto s_wt = [&](int plane, int step) -> float* { return &s_wt_raw[plane * WP + step * WS]; };
     // B/C rows of the chunk, [step][n / SPL][B x SPL, C x SPL]: a lane reads its B and C with one access
     __shared__ __align__(16) float s_bc[TC][2 * NS];
-    // wave-private slabs of g_t (plane 0) and h_t (plane 1): [wave][plane][slot][state block][channel][VB],
-    // a (slot, block) row holding the VB states of the block for every channel of the wave, rows packed
-    // and plane 1 starting 4 floats past a multiple of 8. Measured on gfx950 (N=16, 8 lanes per channel):
-    // the deposits (ds_write_b64 by lane (channel, block) into row block, column channel) then run
-    // without bank conflicts, and so do the fold's ds_read_b128 of whole rows when the lanes of rows 4..7
-    // of a group take the row's four 16-byte pieces in the order 2, 3, 0, 1 (see the fold)
-    constexpr int RW = CPW * VB;
-    constexpr int PL = kRedSlots * 8 * RW + 4;
+    // wave-private slabs of the weighted channel-pair sums of g_t (plane 0) and h_t (plane 1):
+    // [wave][plane][slot][state block][channel pair][VB], a (slot, block) row holding the block's VB
+    // states for every channel pair. Rows are packed and plane 1 starts 16 floats past a multiple of 64:
+    // measured on gfx950 (N=16, 8 lanes per channel: rows of 8 floats), the deposits (ds_write_b64, the
+    // two planes' lanes interleaved) are then conflict-free, and so are the fold's two ds_read_b128 of a
+    // row when plane 1's lanes read the row's halves in swapped order (see the fold)
+    constexpr int RW = NPC * VB;
+    constexpr int PL = kRedSlots * 8 * RW + 16;
     __shared__ __align__(16) float s_red[4][2 * PL];
     auto s_in = [&](int plane, int ch) -> float* { return &s_in_raw[plane * AS + ch * RS]; };
     __shared__ __align__(16) float s_part[4][TC][2 * NS];
@@ -365,10 +364,12 @@ ssm_bwd_kernel(
     const int64_t row0 = (int64_t)b * L;
 
     // folding roles: slot rs (step i+rs), plane rpl (0: dB from g, 1: dC from h), state block rb; with
-    // rows of 8 channels x 2 states, lanes rb >= 4 read their row's halves in swapped order (frot)
+    // rows of two 16-byte halves, plane 1's lanes read them in swapped order
     const int rs = lane >> 4, rpl = (lane >> 3) & 1, rb = lane & 7;
-    constexpr bool kFoldRot = CPW == 8 && VB == 2;
-    const int frot = kFoldRot ? rb >> 2 : 0;
+    constexpr bool kFoldRot = NPC * VB == 8;
+    // depositing role: plane (the g sums on lanes whose bit PB is 0) and channel-pair column
+    const int dpl = (lane >> PB) & 1;
+    const int cwp = (cw & ((1 << PB) - 1)) | ((cw >> (PB + 1)) << PB);
 
     float A2[SPL], An[SPL], gc[SPL], dAacc[SPL];
 #pragma unroll
@@ -497,11 +498,6 @@ ssm_bwd_kernel(
         stv<SPG>((s_in(1, lc) + sg * SPG), vdu);
         stv<SPG>((s_in(2, lc) + sg * SPG), vy);
 #pragma unroll
-        for (int s = 0; s < SPG; ++s) {  // the fold's weights, transposed
-            s_wt(0, sg * SPG + s)[lc] = vdu[s];
-            s_wt(1, sg * SPG + s)[lc] = vy[s];
-        }
-#pragma unroll
         for (int q = 0; q < BCPT; ++q) {
             const int e = tid * BCPT + q;
             if (BCN >= 256 || e < BCN) {
@@ -582,32 +578,26 @@ ssm_bwd_kernel(
         // B/C are read one step ahead and delta/dout one 4-step group ahead of use; every 4 steps the
         // wave folds the phase's deposits over its channels.
         auto fold = [&](int phase) {
-            // this lane's (slot, plane, block) row: the block's VB states for each of the CPW channels
-            float v[CPW * VB], w[CPW], acc[VB];
+            // this lane's (slot, plane, block) row: the block's VB weighted sums for each channel pair
+            float v[NPC * VB], acc[VB];
             const float* row = (rpl ? red_h : red_g) + (rs * 8 + rb) * RW;
-            const float* wrow = s_wt(rpl, phase * kRedSlots + rs) + wave * CPW;
             if constexpr (kFoldRot) {
-                // rows of 16 floats (8 channels x 2 states): lanes rb >= 4 read the halves of the row, and
-                // of the weights, swapped; channel order does not matter to the sum
-                ldv<8>(row + 8 * frot, *reinterpret_cast<float(*)[8]>(v));
-                ldv<8>(row + 8 - 8 * frot, *reinterpret_cast<float(*)[8]>(v + 8));
-                ldv<4>(wrow + 4 * frot, *reinterpret_cast<float(*)[4]>(w));
-                ldv<4>(wrow + 4 - 4 * frot, *reinterpret_cast<float(*)[4]>(w + 4));
+                ldv<4>(row + 4 * rpl, *reinterpret_cast<float(*)[4]>(v));
+                ldv<4>(row + 4 - 4 * rpl, *reinterpret_cast<float(*)[4]>(v + 4));
             } else {
-                ldv<CPW * VB>(row, v);
-                ldv<CPW>(wrow, w);
+                ldv<NPC * VB>(row, v);
             }
 #pragma unroll
-            for (int q = 0; q < VB; ++q) acc[q] = v[q] * w[0];
+            for (int q = 0; q < VB; ++q) acc[q] = v[q];
 #pragma unroll
-            for (int ch = 1; ch < CPW; ++ch) {
+            for (int p = 1; p < NPC; ++p) {
 #pragma unroll
-                for (int q = 0; q < VB; ++q) acc[q] = __builtin_fmaf(v[ch * VB + q], w[ch], acc[q]);
+                for (int q = 0; q < VB; ++q) acc[q] += v[p * VB + q];
             }
             stv<VB>(&s_part[wave][phase * kRedSlots + rs][rpl * NS + rb * VB], acc);
         };
         {
-            float yq[4], dq[4], yqn[4], dqn[4], Bn[SPL], Cn[SPL];
+            float yq[4], dq[4], uq[4], yqn[4], dqn[4], uqn[4], Bn[SPL], Cn[SPL];
             // The group sums over n of each step, S1 = sum g*B (for du) and S2 = sum g*A*dA*h_{t-1} (with
             // u*S1, ddelta), are reduce-scattered over the group every RST steps: the lane's partials of
             // RST steps x (S1, S2) go in, and the lane writes the one (step, sum) the scatter leaves it.
@@ -618,6 +608,7 @@ ssm_bwd_kernel(
             float* const s_mine = &s_out[ridx & 1][ridx >> 1][c];  // + the round's first step * OS
             ldv<4>(s_in(2, c) + TC - 4, yqn);
             ldv<4>(s_in(0, c) + TC - 4, dqn);
+            ldv<4>(s_in(1, c) + TC - 4, uqn);
             auto ld_bc = [&](int i, float (&Bo)[SPL], float (&Co)[SPL]) {
                 float bc[2 * SPL];
                 ldv<2 * SPL>(&s_bc[i][2 * n0], bc);
@@ -636,10 +627,12 @@ ssm_bwd_kernel(
                     for (int q = 0; q < 4; ++q) {
                         yq[q] = yqn[q];
                         dq[q] = dqn[q];
+                        uq[q] = uqn[q];
                     }
                     if (i >= 4) {
                         ldv<4>(s_in(2, c) + i - 7, yqn);
                         ldv<4>(s_in(0, c) + i - 7, dqn);
+                        ldv<4>(s_in(1, c) + i - 7, uqn);
                     }
                 }
                 float Bv[SPL], Cv[SPL];
@@ -654,7 +647,7 @@ ssm_bwd_kernel(
                 // keep the next step's operand reads here, a full step ahead of their use (the
                 // scheduler would otherwise sink them next to the use and expose the LDS latency)
                 __builtin_amdgcn_sched_barrier(0);
-                const float yo = yq[slot], dti = dq[slot];
+                const float yo = yq[slot], dti = dq[slot], dtui = uq[slot];
                 float gt[SPL];
                 float r1 = 0.f, r2 = 0.f;
 #pragma unroll
@@ -670,19 +663,24 @@ ssm_bwd_kernel(
                 rp[2 * (i % RST)] = r1;
                 rp[2 * (i % RST) + 1] = r2;
                 if (i % RST == 0) s_mine[i * OS] = reduce_scatter_hi<CPW, RV>(rp);
-                // deposit g_t and h_t: state n goes to row (slot, n / VB), column cw * VB + n % VB
+                // dB/dC: weight g_t by delta*u and h_t by dout, add the channel partner's, deposit the side
+                // this lane keeps: state n goes to row (slot, n / VB), column cwp * VB + n % VB
+                float pw[2 * SPL], dv[SPL];
+#pragma unroll
+                for (int j = 0; j < SPL; ++j) {
+                    pw[2 * j] = gt[j] * dtui;
+                    pw[2 * j + 1] = H[i][j] * yo;
+                }
+                pair_level<PB, SPL>(pw, dv, lane);
                 constexpr int DW = SPL < VB ? SPL : VB;  // floats per deposit write
+                float* const dep = dpl ? red_h : red_g;
 #pragma unroll
                 for (int j0 = 0; j0 < SPL; j0 += DW) {
-                    const int n = n0 + j0, o = (slot * 8 + n / VB) * RW + cw * VB + n % VB;
-                    float wg[DW], wh[DW];
+                    const int n = n0 + j0, o = (slot * 8 + n / VB) * RW + cwp * VB + n % VB;
+                    float wv[DW];
 #pragma unroll
-                    for (int q = 0; q < DW; ++q) {
-                        wg[q] = gt[j0 + q];
-                        wh[q] = H[i][j0 + q];
-                    }
-                    stv<DW>(red_g + o, wg);
-                    stv<DW>(red_h + o, wh);
+                    for (int q = 0; q < DW; ++q) wv[q] = dv[j0 + q];
+                    stv<DW>(dep + o, wv);
                 }
                 if (slot == 0) {
                     wave_lds_fence();
