@@ -8,6 +8,9 @@ all inputs resident in HBM. Prints ONE JSON line.
 
   python bench.py [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4a|cfg4b]
                   [--level 0|1] [--skip-cpu] [--transforms] [--decode [BATCH]] [--shard K]
+                  [--nstate 8|16|32|64] [--dtype f16|bf16|f32]
+  python bench.py --profile-recipe DIR   # the rocprofv3 commands behind profiles/*.txt
+  python bench.py --summarize DIR        # their CSV output -> profiles/*.txt (no GPU needed)
 
 `value` = B*L*D / ms_per_step (elements/s). `roofline` covers the dominant
 kernel (the fused backward call), timed live with HIP events on the stream
@@ -87,19 +90,31 @@ def _events_ms(fn, n):
     return a.elapsed_time(b) / n
 
 
-def bench_ssm(cfg, steps, warmup, level, shard=1):
+DTYPES = {"f16": "float16", "bf16": "bfloat16", "f32": "float32"}
+
+
+def _pmc_field(name, key):
+    """A figure from a committed rocprofv3 --pmc summary (profiles/<name>_pmc.txt), or None."""
+    path = os.path.join(ROOT, "profiles", f"{name}_pmc.txt")
+    if not os.path.exists(path):
+        return None
+    m = re.search(rf"^{key}:\s*([0-9.eE+-]+)", open(path).read(), re.M)
+    return float(m.group(1)) if m else None
+
+
+def bench_ssm(cfg, steps, warmup, level, shard=1, nstate=16, dtype_name=None):
     import torch
 
     from mamba_windows_cuda import SelectiveScanCuda, ops, workloads
 
     c = workloads.CONFIGS[cfg]
     B, L, D = c["B"], c["L"], c["D"] // shard
-    dtype = c["dtype"]
-    if shard == 1:
+    dtype = getattr(torch, DTYPES[dtype_name]) if dtype_name else c["dtype"]
+    if shard == 1 and nstate == 16 and dtype == c["dtype"]:
         x = workloads.config_inputs(cfg, device="cuda", gen_device="cuda")
-    else:  # one GPU's channels when D is split over `shard` GPUs
-        kw = {k: v for k, v in c.items() if k not in ("B", "L", "D")}
-        x = workloads.ssm_inputs(B, L, D, device="cuda", gen_device="cuda", **kw)
+    else:  # one GPU's channels when D is split over `shard` GPUs, or another state count / dtype
+        kw = {k: v for k, v in c.items() if k not in ("B", "L", "D", "dtype")}
+        x = workloads.ssm_inputs(B, L, D, device="cuda", gen_device="cuda", dtype=dtype, nstate=nstate, **kw)
     leaves = {k: x[k].requires_grad_(True) for k in ("u", "delta", "A", "B", "C", "D")}
     dout = x["dout"]
     m = SelectiveScanCuda(checkpoint_lvl=level)
@@ -141,33 +156,50 @@ def bench_ssm(cfg, steps, warmup, level, shard=1):
         fwd_ms = _events_ms(fwd, n_k)
         bwd_ms = _events_ms(bwd, n_k)
 
-    s = 2 if dtype == torch.float16 else 4
-    bytes_fwd = workloads.algorithmic_bytes(B, L, D, s, fwd=True, bwd=False)
-    bytes_bwd = workloads.algorithmic_bytes(B, L, D, s, fwd=False, bwd=True)
+    s = torch.tensor([], dtype=dtype).element_size()
+    bytes_fwd = workloads.algorithmic_bytes(B, L, D, s, fwd=True, bwd=False, nstate=nstate)
+    bytes_bwd = workloads.algorithmic_bytes(B, L, D, s, fwd=False, bwd=True, nstate=nstate)
     elems = B * L * D
+    states = elems * nstate
     gbs_bwd = bytes_bwd / (bwd_ms * 1e-3) / 1e9
     gbs_step = (bytes_fwd + bytes_bwd) / (ms * 1e-3) / 1e9
+    default_case = shard == 1 and nstate == 16 and dtype == c["dtype"]
+    # HBM bytes the counters measured for one backward call (committed rocprofv3 --pmc summary), and the
+    # VALU instructions its main kernel issued per state and step (SQ_INSTS_VALU x 64 lanes / states)
+    traffic = _traffic_from_profiles(f"ssm_bwd_{cfg}") if default_case else None
+    valu_instr = _pmc_field(f"ssm_bwd_{cfg}", "main_kernel_valu_instructions_per_state_step") if default_case else None
+    valu_instr_fwd = _pmc_field(f"ssm_fwd_{cfg}", "main_kernel_valu_instructions_per_state_step") if default_case else None
+    sdt = {torch.float16: "f16", torch.bfloat16: "bf16"}.get(dtype, "f32")
     res = {
         "metric": METRIC,
         "value": elems / (ms * 1e-3),
         "unit": "elements/s",
         "ms_per_step": ms,
         "dtype": "f32",
-        "storage_dtype": "f16" if s == 2 else "f32",
-        "config": {"workload": f"{cfg}: selective scan fwd+bwd (fused), B={B} L={L} D={D} N=16, "
+        "storage_dtype": sdt,
+        "config": {"workload": f"{cfg}: selective scan fwd+bwd (fused), B={B} L={L} D={D} N={nstate}, "
                                f"checkpoint_lvl={level}"
+                               + (f", {sdt} storage" if dtype != c["dtype"] else "")
                                + (f"; one GPU's share of D={c['D']} split over {shard} GPUs" if shard > 1 else ""),
-                   "B": B, "L": L, "D": D, "N": 16, "checkpoint_lvl": level},
+                   "B": B, "L": L, "D": D, "N": nstate, "checkpoint_lvl": level},
+        # achieved = algorithmic (useful) bytes / call time; traffic = what the counters measured moving
         "roofline": {"bound": "hbm", "kernel": "ssm_bwd (fused backward call)",
                      "achieved": gbs_bwd, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": gbs_bwd / HBM_PEAK_GBS, "traffic": _traffic_from_profiles(f"ssm_bwd_{cfg}") if shard == 1 else None,
-                     "algorithmic_bytes_per_launch": bytes_bwd, "avg_launch_ms": bwd_ms},
+                     "frac": gbs_bwd / HBM_PEAK_GBS, "traffic": traffic,
+                     "algorithmic_bytes_per_launch": bytes_bwd, "avg_launch_ms": bwd_ms,
+                     "achieved_counts": "useful (algorithmic) bytes",
+                     "traffic_GBps": traffic / (bwd_ms * 1e-3) / 1e9 if traffic else None,
+                     "traffic_frac": traffic / (bwd_ms * 1e-3) / 1e9 / HBM_PEAK_GBS if traffic else None,
+                     "limiter": "VALU issue (SQ counters: the SIMDs are VALU-busy most of the waves' lifetime; "
+                                "HBM and LDS are not saturated)"},
         "valu_roofline": {"bound": "valu", "kernel": "ssm_bwd (fused backward call)",
-                          "achieved": B * L * D * 16 * VALU_SLOTS_BWD / (bwd_ms * 1e-3) / 1e12,
+                          "achieved": states * VALU_SLOTS_BWD / (bwd_ms * 1e-3) / 1e12,
                           "peak": VALU_PEAK_TOPS, "unit": "T lane-op/s",
-                          "frac": B * L * D * 16 * VALU_SLOTS_BWD / (bwd_ms * 1e-3) / 1e12 / VALU_PEAK_TOPS,
+                          "frac": states * VALU_SLOTS_BWD / (bwd_ms * 1e-3) / 1e12 / VALU_PEAK_TOPS,
                           "slots_per_state": VALU_SLOTS_BWD,
-                          "fwd_frac": B * L * D * 16 * VALU_SLOTS_FWD / (fwd_ms * 1e-3) / 1e12 / VALU_PEAK_TOPS},
+                          "fwd_frac": states * VALU_SLOTS_FWD / (fwd_ms * 1e-3) / 1e12 / VALU_PEAK_TOPS,
+                          "measured_valu_instr_per_state_step_bwd_main": valu_instr,
+                          "measured_valu_instr_per_state_step_fwd_main": valu_instr_fwd},
         "kernels": {"ssm_fwd_ms": fwd_ms, "ssm_bwd_ms": bwd_ms,
                     "fwd_algorithmic_GBps": bytes_fwd / (fwd_ms * 1e-3) / 1e9},
         "step_hbm": {"algorithmic_bytes": bytes_fwd + bytes_bwd, "achieved_GBps": gbs_step,
@@ -177,7 +209,7 @@ def bench_ssm(cfg, steps, warmup, level, shard=1):
         "retained_after_forward_GB": kept / 1e9,
     }
     if shard > 1:  # what the shards would exchange: one all-reduce of the dB/dC partials (fp32)
-        res["shard"] = {"gpus": shard, "split": "D", "allreduce_bytes": 2 * B * L * 16 * 4}
+        res["shard"] = {"gpus": shard, "split": "D", "allreduce_bytes": 2 * B * L * nstate * 4}
     return res
 
 
@@ -322,11 +354,13 @@ def bench_stream(steps, warmup):
     }
 
 
-def cpu_baseline(cfg, d_frac=2):
+def cpu_baseline(cfg, d_frac=2, runs=3):
     """Plain-PyTorch restatement of the reference's CPU path, structured like
     selective_scan_ref (mamba_cuda.py:875-946: (B,D,N,L) dA/dBu then a loop
-    over L) with torch autograd for the backward, fp32, timed on a bounded
-    sample of the workload: batch row 0, full L, the first D/d_frac channels."""
+    over L) with torch autograd for the backward, in the config's dtype (torch's
+    CPU kernels run fp16 elementwise work natively), timed on a bounded sample of
+    the workload: batch row 0, full L, the first D/d_frac channels; the median of
+    `runs` timed runs after one warm-up call."""
     import torch
 
     from mamba_windows_cuda import workloads
@@ -336,7 +370,7 @@ def cpu_baseline(cfg, d_frac=2):
     torch.set_num_threads(cores)
     c = workloads.CONFIGS[cfg]
     L, D = c["L"], c["D"] // d_frac
-    x = workloads.ssm_inputs(1, L, D, dtype=torch.float32, a_lo=c["a_lo"], a_hi=c["a_hi"], d_mode=c["d_mode"])
+    x = workloads.ssm_inputs(1, L, D, dtype=c["dtype"], a_lo=c["a_lo"], a_hi=c["a_hi"], d_mode=c["d_mode"])
 
     def once(n):
         leaves = [x[k][:, :n].clone().requires_grad_(True) if x[k].dim() == 3 else x[k].clone().requires_grad_(True)
@@ -345,13 +379,18 @@ def cpu_baseline(cfg, d_frac=2):
         out.backward(x["dout"][:, :n])
 
     once(16)  # load the CPU kernels
-    t = time.perf_counter()
-    once(L)
-    per = time.perf_counter() - t
+    times = []
+    for _ in range(runs):
+        t = time.perf_counter()
+        once(L)
+        times.append(time.perf_counter() - t)
+    per = sorted(times)[len(times) // 2]
+    sdt = "fp16" if c["dtype"] == torch.float16 else "fp32"
     return {"value": L * D / per, "unit": "elements/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"{cfg} batch row 0, L={L}, first {D} of {c['D']} channels, fp32, forward + autograd "
-                      f"backward of the selective_scan_ref-structured restatement, 1 timed run of {per:.1f} s; "
-                      f"os.cpu_count()={os.cpu_count()}, affinity={cores}"}
+            "sample": f"{cfg} batch row 0, L={L}, first {D} of {c['D']} channels, {sdt}, forward + autograd "
+                      f"backward of the selective_scan_ref-structured restatement; median of {runs} runs "
+                      f"({', '.join(f'{t:.1f}' for t in times)} s); os.cpu_count()={os.cpu_count()}, "
+                      f"affinity={cores}"}
 
 
 def kernels_only(cfg):
@@ -379,6 +418,178 @@ def kernels_only(cfg):
     return {"mode": "kernels-only", "config": cfg, "calibration_copy_bytes": src.numel() * 4}
 
 
+# rocprofv3 runs behind the committed summaries in profiles/ (bench.py arguments per kernel-trace run;
+# counter passes over `bench.py --kernels-only`). `--profile-recipe DIR` prints the commands, `--summarize
+# DIR` turns their CSV output into profiles/*.txt.
+TRACE_RUNS = {
+    "cfg2_fwd_bwd": ["--skip-cpu"],
+    "cfg3_level0": ["--config", "cfg3", "--level", "0", "--skip-cpu", "--steps", "30"],
+    "cfg3_level1": ["--config", "cfg3", "--level", "1", "--skip-cpu", "--steps", "30"],
+    "cfg4a_stream": ["--config", "cfg4a", "--steps", "10"],
+    "cfg4b_pscan": ["--config", "cfg4b", "--steps", "50"],
+    "decode_b1024": ["--decode", "1024", "--steps", "320"],
+}
+PMC_PASSES = {
+    "fetch": "FETCH_SIZE",
+    "write": "WRITE_SIZE",
+    "sq1": "SQ_WAVE_CYCLES SQ_INSTS_VALU SQ_INSTS_LDS SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_LDS SQ_WAIT_INST_LDS "
+           "SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE",
+    "sq2": "SQ_WAIT_INST_ANY SQ_WAIT_ANY SQ_ACTIVE_INST_ANY SQ_INSTS_SALU SQ_BUSY_CYCLES SQ_WAVES SQ_INSTS_VMEM "
+           "SQ_INSTS_SMEM",
+}
+# one call of each fused operation in the --kernels-only run: (summary name, kernels of the call, the main
+# kernel whose SQ counters are listed, algorithmic bytes, state-steps for the VALU count, description)
+PMC_CALLS = (
+    ("ssm_bwd_cfg2", r"ssm_bwd_carry_kernel|ssm_bwd_kernel|bwd_finish_kernel", r"ssm_bwd_kernelI",
+     2 * (5 * 8 * 2048 * 1536 + 4 * 8 * 2048 * 16 + 2 * 1536 * 16 + 2 * 1536), 8 * 2048 * 1536 * 16,
+     "fused backward call at cfg2 (carry, main and finish kernels)"),
+    ("ssm_fwd_cfg2", r"ssm_fwd_kernel", r"ssm_fwd_kernelIDF16_Li16ELi2ELi0E",
+     2 * (3 * 8 * 2048 * 1536 + 2 * 8 * 2048 * 16 + 1536 * 16 + 1536), 8 * 2048 * 1536 * 16,
+     "fused forward call with checkpoints at cfg2 (carry and main kernels)"),
+    ("pscan_cfg4b", r"pscan_kernel|pscan_clear_kernel", r"pscan_kernel", 3 * 4 * 4 * 65536 * 1024, None,
+     "parallel_scan_fn at cfg4b (clear and scan kernels)"),
+)
+
+
+def _profile_cmd(out, run, args):
+    return (f"rocprofv3 --kernel-trace --stats -f csv -d {out}/trace_{run} -o run -- python3 {ROOT}/bench.py "
+            + " ".join(args) + f" > {out}/trace_{run}.json")
+
+
+def profile_recipe(out):
+    """The shell commands behind profiles/*.txt (run from /tmp with TMPDIR=/tmp, one GPU)."""
+    lines = ["cd /tmp && export TMPDIR=/tmp"]
+    lines += [_profile_cmd(out, run, args) for run, args in TRACE_RUNS.items()]
+    lines += [f"timeout -s KILL 120 rocprofv3 --pmc {c} -f csv -d {out}/pmc_{n} -o run -- python3 {ROOT}/bench.py "
+              f"--kernels-only" for n, c in PMC_PASSES.items()]
+    lines.append(f"python3 {ROOT}/bench.py --summarize {out}")
+    return lines
+
+
+def _short(k):
+    m = re.search(r"(ssm_fwd_kernel|ssm_bwd_carry_kernel|ssm_bwd_kernel|bwd_finish_kernel|ssm_step_kernel|"
+                  r"pscan_kernel|pscan_clear_kernel|copyBuffer)", k)
+    name = m.group(1) if m else k[:48]
+    if name == "ssm_fwd_kernel":
+        mode = re.search(r"Li\d+ELi\d+ELi(\d)E", k)
+        name += {"0": " (main)", "1": " (state-only)", "2": " (carry)"}.get(mode.group(1) if mode else "", "")
+    return name
+
+
+def _csv_rows(d, suffix):
+    import csv
+    import glob
+
+    rows = []
+    for f in sorted(glob.glob(os.path.join(d, "**", f"*{suffix}"), recursive=True)):
+        rows += list(csv.DictReader(open(f)))
+    return rows
+
+
+def summarize(out, dest=None):
+    """Writes profiles/*.txt from the rocprofv3 CSV output of the profile_recipe() commands in `out`."""
+    import statistics
+
+    dest = dest or os.path.join(ROOT, "profiles")
+    written = []
+    for run, args in TRACE_RUNS.items():
+        d = os.path.join(out, f"trace_{run}")
+        stats = _csv_rows(d, "kernel_stats.csv")
+        if not stats:
+            continue
+        L = ["# rocprofv3 kernel statistics (MI355X, gfx950)",
+             f"command: cd /tmp && export TMPDIR=/tmp && {_profile_cmd('<out>', run, args)}; "
+             f"python3 bench.py --summarize <out>",
+             "kernel | calls | avg_us | min_us | max_us | pct"]
+        avg = {}
+        for r in stats:
+            k = r["Name"]
+            avg[k] = float(r["AverageNs"]) / 1e3
+            L.append(f"{_short(k)} [{k[:60]}] | {r['Calls']} | {avg[k]:.1f} | {float(r['MinNs']) / 1e3:.1f} | "
+                     f"{float(r['MaxNs']) / 1e3:.1f} | {float(r['Percentage']):.2f}")
+        fwd = sum(v for k, v in avg.items() if "ssm_fwd_kernel" in k and re.search(r"ELi[02]ELi\d+EEEv", k))
+        bwd = sum(v for k, v in avg.items() if re.search(r"ssm_bwd_carry_kernel|ssm_bwd_kernel|bwd_finish_kernel", k))
+        if fwd or bwd:
+            L.append(f"fused forward call (carry + main kernels): {fwd:.1f} us; fused backward call (carry + main + "
+                     f"finish kernels): {bwd:.1f} us")
+        bj = os.path.join(out, f"trace_{run}.json")
+        if os.path.exists(bj):
+            try:
+                line = json.loads([x for x in open(bj).read().splitlines() if x.startswith("{")][-1])
+                keep = {k: line[k] for k in ("metric", "value", "unit", "ms_per_step", "us_per_step", "storage_dtype",
+                                             "retained_after_forward_GB", "peak_hbm_allocated_GB", "kernels")
+                        if k in line}
+                if "roofline" in line:
+                    keep["roofline"] = {k: line["roofline"][k] for k in ("achieved", "frac", "avg_launch_ms")
+                                        if k in line["roofline"]}
+                keep["workload"] = line.get("config", {}).get("workload")
+                L.append("bench line under the profiler: " + json.dumps(keep))
+            except (ValueError, IndexError):
+                pass
+        name = f"kernel_trace_{run}.txt"
+        open(os.path.join(dest, name), "w").write("\n".join(L) + "\n")
+        written.append(name)
+
+    # counter passes: per kernel name, the median over its dispatches of each counter (for the copy
+    # kernel, the largest dispatch: the 1 GiB calibration copy, not the small copies of status reads)
+    def pmc(n):
+        per = {}
+        for r in _csv_rows(os.path.join(out, f"pmc_{n}"), "counter_collection.csv"):
+            key = (r["Kernel_Name"], r["Dispatch_Id"])
+            per.setdefault(key, {}).setdefault(r["Counter_Name"], 0.0)
+            per[key][r["Counter_Name"]] += float(r["Counter_Value"])
+        agg = {}
+        for (k, _), cs in per.items():
+            for c, v in cs.items():
+                agg.setdefault(k, {}).setdefault(c, []).append(v)
+        return {k: {c: (max(v) if "copyBuffer" in k else statistics.median(v)) for c, v in cs.items()}
+                for k, cs in agg.items()}
+
+    F, W, S1, S2 = pmc("fetch"), pmc("write"), pmc("sq1"), pmc("sq2")
+    copies = [k for k in F if "copyBuffer" in k]
+    if F and W and copies:
+        copy = copies[0]
+        gib = float(1 << 30)
+        fcal = gib / (F[copy]["FETCH_SIZE"] * 1024)
+        wcal = gib / (W[[k for k in W if "copyBuffer" in k][0]]["WRITE_SIZE"] * 1024)
+        for name, pat, main_pat, alg, nstate_steps, what in PMC_CALLS:
+            ks = [k for k in F if re.search(pat, k)]
+            if not ks:
+                continue
+            fb = sum(F[k]["FETCH_SIZE"] for k in ks) * 1024 * fcal
+            wb = sum(W[k]["WRITE_SIZE"] for k in W if re.search(pat, k)) * 1024 * wcal
+            L = [f"# rocprofv3 --pmc summary (MI355X, gfx950), one {what}",
+                 "command: cd /tmp && export TMPDIR=/tmp && for each pass: timeout -s KILL 120 rocprofv3 --pmc "
+                 "<counters> -f csv -d <out>/pmc_<pass> -o run -- python3 bench.py --kernels-only; then "
+                 "python3 bench.py --summarize <out>. Passes: "
+                 + "; ".join(f"{n}: {c}" for n, c in PMC_PASSES.items()),
+                 f"calibration: a 1 GiB device copy reads FETCH_SIZE={F[copy]['FETCH_SIZE']:.4g} KiB and "
+                 f"WRITE_SIZE={W[[k for k in W if 'copyBuffer' in k][0]]['WRITE_SIZE']:.4g} KiB -> scale FETCH by "
+                 f"{fcal:.3f}, WRITE by {wcal:.3f} (bytes moved = counter KiB x 1024 x scale)",
+                 "kernels: " + ", ".join(sorted({_short(k) for k in ks})),
+                 f"fetch_bytes_per_launch: {fb:.4g}", f"write_bytes_per_launch: {wb:.4g}",
+                 f"traffic_bytes_per_launch: {fb + wb:.6g}", f"algorithmic_bytes_per_launch: {alg}",
+                 f"traffic_over_algorithmic: {(fb + wb) / alg:.3f}"]
+            mains = [k for k in S1 if re.search(main_pat, k)]
+            if mains:
+                m = mains[0]
+                sq = dict(S1[m])
+                sq.update(S2.get([k for k in S2 if re.search(main_pat, k)][0], {}) if S2 else {})
+                L.append(f"SQ counters of {_short(m)}: " + ", ".join(f"{c}={v:.4g}" for c, v in sorted(sq.items())))
+                wc = sq.get("SQ_WAVE_CYCLES")
+                if wc:
+                    L.append(f"per wave-cycle: VALU busy {sq['SQ_ACTIVE_INST_VALU'] / wc:.3f}, LDS busy "
+                             f"{sq['SQ_ACTIVE_INST_LDS'] / wc:.3f}, waiting on LDS {sq['SQ_WAIT_INST_LDS'] / wc:.3f}, "
+                             f"waiting on anything {sq.get('SQ_WAIT_ANY', 0) / wc:.3f}")
+                if nstate_steps:
+                    L.append(f"main_kernel_valu_instructions_per_state_step: "
+                             f"{sq['SQ_INSTS_VALU'] * 64 / nstate_steps:.3f}")
+            fname = f"{name}_pmc.txt"
+            open(os.path.join(dest, fname), "w").write("\n".join(L) + "\n")
+            written.append(fname)
+    return written
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -395,7 +606,21 @@ def main():
                     help="time one GPU's share of the config when D is split over this many GPUs")
     ap.add_argument("--kernels-only", action="store_true",
                     help="profiling driver: fused calls, cfg4b scan and a 1 GiB copy; no timing")
+    ap.add_argument("--nstate", type=int, default=16, choices=[8, 16, 32, 64],
+                    help="state count N of the fwd+bwd step (the reference builds N=16 only)")
+    ap.add_argument("--dtype", default=None, choices=sorted(DTYPES),
+                    help="storage dtype of the fwd+bwd step (default: the config's)")
+    ap.add_argument("--profile-recipe", metavar="DIR", default=None,
+                    help="print the rocprofv3 commands whose output --summarize turns into profiles/*.txt")
+    ap.add_argument("--summarize", metavar="DIR", default=None,
+                    help="write profiles/*.txt from the rocprofv3 CSV output in DIR (no GPU needed)")
     args = ap.parse_args()
+    if args.profile_recipe:
+        print("\n".join(profile_recipe(args.profile_recipe)))
+        return
+    if args.summarize:
+        print(json.dumps({"written": summarize(args.summarize)}))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build measures one GPU only (sharding over GPUs is designed, not "
                                    "built); run with --gpus 1"}))
@@ -420,9 +645,9 @@ def main():
     elif args.config == "cfg4a":
         res = bench_stream(args.steps, args.warmup)
     else:
-        res = bench_ssm(args.config, args.steps, args.warmup, args.level, args.shard)
+        res = bench_ssm(args.config, args.steps, args.warmup, args.level, args.shard, args.nstate, args.dtype)
         res["peak_hbm_allocated_GB"] = torch.cuda.max_memory_allocated() / 1e9
-        if args.shard > 1:
+        if args.shard > 1 or args.nstate != 16 or args.dtype is not None:
             args.skip_cpu = True
     res.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
                 "scaling": "weak", "vs_baseline": None, "data": "synthetic (seeded; BASELINE.json distributions)",

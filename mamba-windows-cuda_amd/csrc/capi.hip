@@ -60,15 +60,17 @@ int mwc_set_hip_error(hipError_t e, const char* what) {
 
 namespace mwc {
 
-// States per lane. Measured on MI355X at B=8, L=2048, D=1536 (fp16): SPL=2 (8 lanes per
-// channel) beats SPL=4 (one wave per SIMD, every stall exposed) and SPL=1 (4x the per-lane
-// overhead of the n-reductions). Small problems use SPL=1 for parallelism.
+// States per lane. Measured on MI355X at B=8, L=2048, D=1536, fp16 fwd+bwd step: at N=16, SPL=2 (8
+// lanes per channel, 0.389 ms) beats SPL=1 (0.464 ms: twice the per-lane overhead of the n-reductions)
+// and SPL=4 (one wave per SIMD); at N=32, SPL=2 takes 0.751 ms and SPL=4 0.966 ms (its forward needs
+// 267 VGPRs, one wave per SIMD); at N=8, SPL=2 takes 0.293 ms and SPL=1 0.330 ms. N=64 is built at
+// SPL=4 only. Small problems use 16 lanes per channel, for parallelism.
 int choose_spl(int64_t channels, int ns) {
     const int o = spl_override();
     if (o && lane_group_supported(ns, o)) return o;
-    // 8 lanes per channel (16 for small problems, for parallelism), within the built set
-    const int spl = ns / (channels >= 2048 ? 8 : 16);
-    return spl < 1 ? 1 : (ns == 64 ? 4 : spl);
+    if (ns == 64) return 4;
+    if (channels >= 2048) return 2;
+    return ns / 16 < 1 ? 1 : ns / 16;
 }
 
 bool lane_group_supported(int ns, int spl) {
@@ -146,12 +148,14 @@ SegPlan plan(const SsmShape& s, bool bwd, int spl, int cap_main, int cap_carry, 
     return best;
 }
 
-// Workgroups per CU each kernel fits, by SPL: min(512 / VGPRs per lane, 160 KB / LDS per
-// workgroup), from the gfx950 build's resource usage.
-int fwd_cap(int spl) { return spl == 1 ? 5 : spl == 2 ? 3 : 1; }
-int fwd_carry_cap(int spl) { return spl == 1 ? 8 : spl == 2 ? 6 : 4; }
-int bwd_cap(int spl) { return spl == 4 ? 1 : 3; }
-int bwd_carry_cap(int spl) { return spl == 1 ? 8 : spl == 2 ? 6 : 4; }
+// Workgroups per CU each kernel fits: the runtime's occupancy query for the instance (registers and LDS
+// of the gfx950 build), or, when no device can be queried, min(512 / VGPRs, 160 KiB / LDS) of the
+// N=16 instances.
+int cap_or(int queried, int fallback) { return queried > 0 ? queried : fallback; }
+int fwd_cap(int ns, int spl) { return cap_or(fwd_wgs_per_cu(ns, spl, 0), spl == 1 ? 7 : spl == 2 ? 3 : 1); }
+int fwd_carry_cap(int ns, int spl) { return cap_or(fwd_wgs_per_cu(ns, spl, 2), spl == 1 ? 8 : spl == 2 ? 6 : 4); }
+int bwd_cap(int ns, int spl) { return cap_or(bwd_wgs_per_cu(ns, spl, false), spl == 1 ? 4 : spl == 2 ? 3 : 1); }
+int bwd_carry_cap(int ns, int spl) { return cap_or(bwd_wgs_per_cu(ns, spl, true), spl == 1 ? 8 : spl == 2 ? 6 : 4); }
 
 size_t carry_bytes(const SsmShape& s, const SegPlan& p) {
     return p.nseg > 1 ? align256((size_t)s.batch * p.ncar * s.dim * s.nstate * sizeof(float)) : 0;
@@ -159,17 +163,14 @@ size_t carry_bytes(const SsmShape& s, const SegPlan& p) {
 
 }  // namespace
 
-// (the tables above are for N=16; other N get a conservative 2, which only steers the segment count)
 SegPlan plan_fwd(const SsmShape& s) {
     const int spl = choose_spl(s.batch * s.dim, s.nstate);
-    const bool n16 = s.nstate == 16;
-    return plan(s, false, spl, n16 ? fwd_cap(spl) : 2, n16 ? fwd_carry_cap(spl) : 2, 0.75);
+    return plan(s, false, spl, fwd_cap(s.nstate, spl), fwd_carry_cap(s.nstate, spl), 0.75);
 }
 
 SegPlan plan_bwd(const SsmShape& s) {
     const int spl = choose_spl(s.batch * s.dim, s.nstate);
-    const bool n16 = s.nstate == 16;
-    return plan(s, true, spl, n16 ? bwd_cap(spl) : 2, n16 ? bwd_carry_cap(spl) : 2, 0.3);
+    return plan(s, true, spl, bwd_cap(s.nstate, spl), bwd_carry_cap(s.nstate, spl), 0.3);
 }
 
 size_t fwd_workspace_bytes(const SsmShape& s) {

@@ -31,6 +31,10 @@ struct SegPlan {
 };
 SegPlan plan_fwd(const SsmShape& s);
 SegPlan plan_bwd(const SsmShape& s);
+// Workgroups per CU of a lane-group kernel instance (the HIP runtime's occupancy query, cached), or 0 when
+// no device can be queried. fwd mode: 0 main, 1 state-only, 2 carry.
+int fwd_wgs_per_cu(int ns, int spl, int mode);
+int bwd_wgs_per_cu(int ns, int spl, bool carry);
 
 // Workspace carve-up (bytes, 256-aligned pieces).
 size_t fwd_workspace_bytes(const SsmShape& s);

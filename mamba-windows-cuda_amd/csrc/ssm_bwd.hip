@@ -38,6 +38,7 @@
 // computes (G, xsum) for every segment but the first, each cut into cfold
 // carry segments; the main kernel folds them, from dh_last, into its starting
 // adjoint.
+#include <atomic>
 #include <type_traits>
 
 #include "common.h"
@@ -827,6 +828,28 @@ __global__ void __launch_bounds__(256) bwd_finish_kernel(const float* __restrict
         const int64_t dd = i - nA - D;
         st(dbias + dd, rows_sum(dbias_part + dd, D));
     }
+}
+
+int bwd_wgs_per_cu(int ns, int spl, bool carry) {
+    // as fwd_wgs_per_cu: the fp16, transform-free instance's occupancy, queried once; 0 if unknown
+    static std::atomic<int> cache[4][3][2];
+    const int ni = ns == 8 ? 0 : ns == 16 ? 1 : ns == 32 ? 2 : 3, si = spl == 1 ? 0 : spl == 2 ? 1 : 2;
+    int v = cache[ni][si][carry].load(std::memory_order_relaxed);
+    if (v != 0) return v < 0 ? 0 : v;
+    const void* k = nullptr;
+#define MWC_BWD_K(N, S)                                                                                   \
+    if (ns == N && spl == S)                                                                              \
+        k = carry ? reinterpret_cast<const void*>(&ssm_bwd_carry_kernel<half_t, N, S, 0>)                 \
+                  : reinterpret_cast<const void*>(&ssm_bwd_kernel<half_t, N, S, 0>);
+    MWC_FOR_EACH_LANE_GROUP(MWC_BWD_K)
+#undef MWC_BWD_K
+    int n = 0;
+    if (k == nullptr || hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, 256, 0) != hipSuccess || n <= 0) {
+        (void)hipGetLastError();
+        n = -1;
+    }
+    cache[ni][si][carry].store(n, std::memory_order_relaxed);
+    return n < 0 ? 0 : n;
 }
 
 int bwd_groups(const SsmShape& s, int ns, int spl) {

@@ -30,6 +30,7 @@
 // padded with delta = u = 0, which leaves the state unchanged, so the inner
 // loop carries no bounds checks. The [-88, 88] clamp of the exponent runs only
 // in chunks where |delta|*max|A| can reach it (a wave-uniform test).
+#include <atomic>
 #include <type_traits>
 
 #include "common.h"
@@ -409,6 +410,30 @@ static hipError_t fwd_inst(const FwdArgs& a, const SsmShape& s, hipStream_t st) 
         case kXfGate: return fwd_inst<T, NS, SPL, kXfGate>(a, s, st);
         default: return fwd_inst<T, NS, SPL, kXfDelta | kXfGate>(a, s, st);
     }
+}
+
+int fwd_wgs_per_cu(int ns, int spl, int mode) {
+    // the runtime's occupancy of the fp16, transform-free instance (registers and LDS differ little
+    // across dtypes and transforms), queried once per (N, SPL, mode); 0 when it cannot be queried
+    static std::atomic<int> cache[4][3][3];
+    const int ni = ns == 8 ? 0 : ns == 16 ? 1 : ns == 32 ? 2 : 3, si = spl == 1 ? 0 : spl == 2 ? 1 : 2;
+    int v = cache[ni][si][mode].load(std::memory_order_relaxed);
+    if (v != 0) return v < 0 ? 0 : v;
+    const void* k = nullptr;
+#define MWC_FWD_K(N, S)                                                                                         \
+    if (ns == N && spl == S)                                                                                    \
+        k = mode == kCarry   ? reinterpret_cast<const void*>(&ssm_fwd_kernel<half_t, N, S, kCarry, 0>)        \
+            : mode == kState ? reinterpret_cast<const void*>(&ssm_fwd_kernel<half_t, N, S, kState, 0>)        \
+                             : reinterpret_cast<const void*>(&ssm_fwd_kernel<half_t, N, S, kMain, 0>);
+    MWC_FOR_EACH_LANE_GROUP(MWC_FWD_K)
+#undef MWC_FWD_K
+    int n = 0;
+    if (k == nullptr || hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, 256, 0) != hipSuccess || n <= 0) {
+        (void)hipGetLastError();
+        n = -1;
+    }
+    cache[ni][si][mode].store(n, std::memory_order_relaxed);
+    return n < 0 ? 0 : n;
 }
 
 hipError_t launch_ssm_fwd(int dt, int ns, int spl, const FwdArgs& a, const SsmShape& s, hipStream_t st) {
