@@ -102,7 +102,24 @@ def _pmc_field(name, key):
     return float(m.group(1)) if m else None
 
 
-def bench_ssm(cfg, steps, warmup, level, shard=1, nstate=16, dtype_name=None):
+def _capture_step(step):
+    """The step captured once in a HIP graph (after eager warm-up steps on a side stream)."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    return graph.replay
+
+
+def bench_ssm(cfg, steps, warmup, level, shard=1, nstate=16, dtype_name=None, graph=False):
     import torch
 
     from mamba_windows_cuda import SelectiveScanCuda, ops, workloads
@@ -135,9 +152,10 @@ def bench_ssm(cfg, steps, warmup, level, shard=1, nstate=16, dtype_name=None):
     kept = torch.cuda.memory_allocated() - base - out_keep.numel() * out_keep.element_size()
     del out_keep
     torch.cuda.reset_peak_memory_stats()
-    warm_run = _warmup(step, warmup)
+    run = _capture_step(step) if graph else step
+    warm_run = _warmup(run, warmup)
     t0 = time.perf_counter()
-    ms_events = _events_ms(step, steps)
+    ms_events = _events_ms(run, steps)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
     ms = max(ms_events, 0.0)
@@ -180,8 +198,9 @@ def bench_ssm(cfg, steps, warmup, level, shard=1, nstate=16, dtype_name=None):
         "config": {"workload": f"{cfg}: selective scan fwd+bwd (fused), B={B} L={L} D={D} N={nstate}, "
                                f"checkpoint_lvl={level}"
                                + (f", {sdt} storage" if dtype != c["dtype"] else "")
-                               + (f"; one GPU's share of D={c['D']} split over {shard} GPUs" if shard > 1 else ""),
-                   "B": B, "L": L, "D": D, "N": nstate, "checkpoint_lvl": level},
+                               + (f"; one GPU's share of D={c['D']} split over {shard} GPUs" if shard > 1 else "")
+                               + ("; the step replayed from a HIP graph" if graph else ""),
+                   "B": B, "L": L, "D": D, "N": nstate, "checkpoint_lvl": level, "graph": graph},
         # achieved = algorithmic (useful) bytes / call time; traffic = what the counters measured moving
         "roofline": {"bound": "hbm", "kernel": "ssm_bwd (fused backward call)",
                      "achieved": gbs_bwd, "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -300,8 +319,8 @@ def bench_decode(cfg, steps, warmup, batch=None):
 
 
 def bench_pscan(steps, warmup):
-    """cfg4b through parallel_scan_fn (value: the API call, which also reads the scan's status word and so
-    waits for the scan) and through the C ABI alone (the roofline: the clear and scan kernels)."""
+    """cfg4b through parallel_scan_fn (value: the API call, including the non-waiting read of the
+    scan's status word) and through the C ABI alone (the roofline: the clear and scan kernels)."""
     import torch
 
     from mamba_windows_cuda import _lib, ops, parallel_scan_fn, workloads
@@ -621,6 +640,8 @@ def main():
                     help="time the scan call with delta_bias/softplus/z gating fused vs. as torch passes")
     ap.add_argument("--shard", type=int, default=1, choices=[1, 2, 4, 8],
                     help="time one GPU's share of the config when D is split over this many GPUs")
+    ap.add_argument("--graph", action="store_true",
+                    help="replay the fwd+bwd step from a HIP graph (no host path per step)")
     ap.add_argument("--kernels-only", action="store_true",
                     help="profiling driver: fused calls, cfg4b scan and a 1 GiB copy; no timing")
     ap.add_argument("--nstate", type=int, default=16, choices=[8, 16, 32, 64],
@@ -662,9 +683,10 @@ def main():
     elif args.config == "cfg4a":
         res = bench_stream(args.steps, args.warmup)
     else:
-        res = bench_ssm(args.config, args.steps, args.warmup, args.level, args.shard, args.nstate, args.dtype)
+        res = bench_ssm(args.config, args.steps, args.warmup, args.level, args.shard, args.nstate, args.dtype,
+                        args.graph)
         res["peak_hbm_allocated_GB"] = torch.cuda.max_memory_allocated() / 1e9
-        if args.shard > 1 or args.nstate != 16 or args.dtype is not None:
+        if args.shard > 1 or args.nstate != 16 or args.dtype is not None or args.graph:
             args.skip_cpu = True
     res.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
                 "scaling": "weak", "vs_baseline": None, "data": "synthetic (seeded; BASELINE.json distributions)",

@@ -197,6 +197,15 @@ int mwc_pscan_bwd(int dtype, const void* A, const void* H, const void* dH, void*
 int mwc_pscan_status(const void* workspace, size_t workspace_bytes, int64_t nseq, int64_t seqlen,
                      int64_t ncols, void* stream);
 
+/*
+ * The same outcome without waiting: enqueues on `stream` a copy of the scan's status word into
+ * `*host_word` (pinned host memory, so the copy does not block the caller) and returns. Once the
+ * stream has passed that point, *host_word is 0 if every wait completed and non-zero if one gave
+ * up (MWC_ERR_INCOMPLETE). No reference counterpart, as mwc_pscan_status.
+ */
+int mwc_pscan_status_async(const void* workspace, size_t workspace_bytes, int64_t nseq, int64_t seqlen,
+                           int64_t ncols, uint32_t* host_word, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

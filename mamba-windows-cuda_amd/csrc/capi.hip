@@ -482,4 +482,20 @@ int mwc_pscan_status(const void* workspace, size_t workspace_bytes, int64_t nseq
     return MWC_OK;
 }
 
+int mwc_pscan_status_async(const void* workspace, size_t workspace_bytes, int64_t nseq, int64_t seqlen,
+                           int64_t ncols, uint32_t* host_word, void* stream) {
+    g_err[0] = 0;
+    if (host_word == nullptr) return fail(MWC_ERR_INVALID_ARGUMENT, "host_word must not be NULL");
+    if (nseq <= 0 || seqlen <= 0 || ncols <= 0) {  // nothing was scanned
+        *host_word = 0;
+        return MWC_OK;
+    }
+    const size_t need = mwc::pscan_workspace_bytes(nseq, seqlen, ncols);
+    if (workspace == nullptr || workspace_bytes < need)
+        return fail(MWC_ERR_WORKSPACE, "scan workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+    MWC_HIP_TRY(hipMemcpyAsync(host_word, (const char*)workspace + mwc::pscan_error_word_offset(nseq, seqlen, ncols),
+                               sizeof(uint32_t), hipMemcpyDeviceToHost, (hipStream_t)stream));
+    return MWC_OK;
+}
+
 }  // extern "C"

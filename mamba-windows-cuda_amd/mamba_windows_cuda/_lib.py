@@ -57,6 +57,7 @@ _SIGNATURES = {
     "mwc_pscan_bwd": ([ctypes.c_int, P, P, P, P, P, I64, I64, I64, P, SZ, P], ctypes.c_int),
     # workspace, bytes, nseq, seqlen, ncols, stream
     "mwc_pscan_status": ([P, SZ, I64, I64, I64, P], ctypes.c_int),
+    "mwc_pscan_status_async": ([P, SZ, I64, I64, I64, P, P], ctypes.c_int),
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -10,6 +10,7 @@ before any device work is queued.
 """
 from __future__ import annotations
 
+import collections
 import functools
 import os
 
@@ -308,18 +309,63 @@ def _check_scan(*ts):
         _require(t.device == ts[0].device, "parallel_scan_fn inputs must share a device")
 
 
+# Status words of recent scans, read without waiting for the GPU: each call enqueues a copy of its
+# scan's status word into pinned host memory plus an event, and every later call (or pscan_check())
+# looks at the words whose events have completed. A bounded look-back wait that gave up (its tiles'
+# outputs are NaN) is so reported by the first scan call, or pscan_check(), after it finished.
+_pending_status = collections.deque()  # (event, pinned int32 word, what)
+_MAX_PENDING = 256
+
+
 def _pscan_status(L_, ws, nbytes, nseq, L, nc, dev, what):
-    """Raise if a bounded look-back wait of the scan just enqueued gave up (its outputs are then NaN).
-    Waits for the stream; skipped while a graph is being captured, where waiting is not allowed."""
+    """Enqueue the read of the status word of the scan just enqueued (skipped while a graph is being
+    captured: the word is then never read)."""
     if torch.cuda.is_current_stream_capturing():
         return
+    word = torch.empty(1, dtype=torch.int32, pin_memory=True)
     with _on_device(dev):
-        st = L_.mwc_pscan_status(ws.data_ptr(), nbytes, nseq, L, nc, _stream(dev))
-    _lib.check(st, what)
+        st = L_.mwc_pscan_status_async(ws.data_ptr(), nbytes, nseq, L, nc, word.data_ptr(), _stream(dev))
+        _lib.check(st, what)
+        ev = torch.cuda.Event()
+        ev.record()
+    _pending_status.append((ev, word, what))
+    if len(_pending_status) > _MAX_PENDING:
+        _drain_status(wait_oldest=True)
+
+
+def _drain_status(wait_all=False, wait_oldest=False):
+    """Retire the status words whose scans have finished (all of them, waiting, with wait_all) and
+    raise RuntimeError if one of them reports a wait that gave up. Nothing is queried while a graph
+    is being captured (event queries are not allowed then)."""
+    if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+        return
+    failed = None
+    first = True
+    while _pending_status:
+        ev, word, what = _pending_status[0]
+        if wait_all or (wait_oldest and first):
+            ev.synchronize()
+        elif not ev.query():
+            break
+        first = False
+        _pending_status.popleft()
+        if int(word[0]) != 0 and failed is None:
+            failed = what
+    if failed is not None:
+        raise RuntimeError(f"{failed} failed: MWC_ERR_INCOMPLETE: a look-back wait of an earlier parallel scan "
+                           "ran out of spins, so the affected tiles' outputs are NaN")
+
+
+def pscan_check():
+    """Wait for every scan enqueued so far and raise RuntimeError (MWC_ERR_INCOMPLETE) if one of them
+    gave up a look-back wait. Scan calls already report such a failure once it has finished, at the
+    next call; this makes the report immediate."""
+    _drain_status(wait_all=True)
 
 
 def pscan_forward(A, X):
     _check_scan(A, X)
+    _drain_status()
     A, X = A.contiguous(), X.contiguous()
     a3, x3 = _scan_view(A), _scan_view(X)
     H = torch.empty_like(X)
@@ -338,6 +384,7 @@ def pscan_forward(A, X):
 
 def pscan_backward(A, H, dH):
     _check_scan(A, H, dH)
+    _drain_status()
     A, H, dH = A.contiguous(), H.contiguous(), dH.contiguous()
     dA = torch.empty_like(A)
     dX = torch.empty_like(A)

@@ -38,6 +38,13 @@ def parallel_scan_fn(A, X):
     return PScan.apply(A, X)
 
 
+def pscan_check():
+    """Wait for the scans enqueued so far and raise RuntimeError if a bounded look-back wait in one of
+    them gave up (its outputs are then NaN). Not in the reference, whose PScan has no waits: scan
+    calls report such a failure without waiting, at the first call after it finished."""
+    ops.pscan_check()
+
+
 def parallel_scan_ref(A, X):
     """Sequential reference scan (pscan.py:153-171): plain PyTorch, any device,
     accumulating in the input dtype. Accepts (B, D, L, N) or (B, L, C)."""

@@ -68,6 +68,11 @@ def test_argument_errors_before_any_launch():
     # empty problems are no-ops
     assert L.mwc_ssm_fwd(0, None, None, fake, None, None, fake, None, None, None, None, 0, 8, 8, 16, None, 0, None) == 0
     assert L.mwc_pscan_fwd(0, None, None, None, 0, 8, 8, None, 0, None) == 0
+    # the non-waiting scan status: no host word, workspace too small; an empty scan reports 0 at once
+    word = ctypes.c_uint32(7)
+    assert L.mwc_pscan_status_async(fake, 1 << 20, 1, 8, 8, None, None) == 1
+    assert L.mwc_pscan_status_async(fake, 4, 2, 1000, 64, ctypes.byref(word), None) == 3
+    assert L.mwc_pscan_status_async(None, 0, 0, 8, 8, ctypes.byref(word), None) == 0 and word.value == 0
 
 
 def test_transform_entry_points_argument_errors():

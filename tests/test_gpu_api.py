@@ -77,18 +77,29 @@ def test_pscan_adjoint_config4b_length(dev):
 
 def test_pscan_wait_give_up_is_reported(dev, monkeypatch):
     """A look-back wait that runs out of polls is an error, not a silently wrong H: with a limit of 0
-    every wait gives up at once (each kernel still runs to its end), the host reports
-    MWC_ERR_INCOMPLETE, and the tiles that waited hold NaN. The default limit gives status OK."""
+    every wait gives up at once (each kernel still runs to its end) and the tiles that waited hold
+    NaN. The scan calls read their status words without waiting: pscan_check() reports the failure
+    at once, and the first scan call after it finished reports it too. The default limit gives OK."""
+    from mamba_windows_cuda import _lib, ops
+    from mamba_windows_cuda.pscan import pscan_check
+
     a, b = workloads.pscan_inputs((2, 1000, 64), seed=5)
     ad, bd = a.to(dev), b.to(dev)
-    H = parallel_scan_fn(ad, bd)  # default limit: completes, status checked inside
+    H = parallel_scan_fn(ad, bd)  # default limit: completes
+    pscan_check()
     np.testing.assert_allclose(_np(H), orc.pscan_fwd(a, b), rtol=1e-3, atol=1e-4)
-    from mamba_windows_cuda import _lib, ops
 
     monkeypatch.setenv("MWC_PSCAN_SPIN_LIMIT", "0")
+    Hbad = parallel_scan_fn(ad, bd)  # enqueued; its status word is read without waiting
     with pytest.raises(RuntimeError, match="MWC_ERR_INCOMPLETE"):
-        parallel_scan_fn(ad, bd)
-    # the raw C ABI: same outcome, and the first tile (no predecessor) is exact while later ones are NaN
+        pscan_check()
+    assert torch.isnan(Hbad[:, 128:]).all()
+    parallel_scan_fn(ad, bd)
+    torch.cuda.synchronize()
+    with pytest.raises(RuntimeError, match="MWC_ERR_INCOMPLETE"):
+        parallel_scan_fn(ad, bd)  # reports the finished failure of the call before
+    # the raw C ABI: the waiting and the non-waiting status reads; the first tile (no predecessor) is
+    # exact while later ones are NaN
     L_ = _lib.lib()
     nbytes = L_.mwc_pscan_workspace_size(2, 1000, 64)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
@@ -96,12 +107,17 @@ def test_pscan_wait_give_up_is_reported(dev, monkeypatch):
     st = L_.mwc_pscan_fwd(_lib.MWC_DTYPE_F32, ad.data_ptr(), bd.data_ptr(), Hc.data_ptr(), 2, 1000, 64,
                           ws.data_ptr(), nbytes, ops._stream(ad.device))
     assert st == 0
+    word = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+    assert L_.mwc_pscan_status_async(ws.data_ptr(), nbytes, 2, 1000, 64, word.data_ptr(),
+                                     ops._stream(ad.device)) == 0
     assert L_.mwc_pscan_status(ws.data_ptr(), nbytes, 2, 1000, 64, ops._stream(ad.device)) == 5
+    assert int(word[0]) != 0
     Hc = Hc.cpu()
     assert torch.isnan(Hc[:, 128:]).all()
     torch.testing.assert_close(Hc[:, :128], H[:, :128].cpu(), rtol=0, atol=0)
     monkeypatch.delenv("MWC_PSCAN_SPIN_LIMIT")
     Hd = parallel_scan_fn(ad, bd)  # the next call with the default limit clears the word and completes
+    pscan_check()
     # (not bitwise: a tile's prefix sums its predecessors' aggregates or takes an inclusive prefix,
     # whichever is published when it looks, so the rounding order varies from run to run)
     torch.testing.assert_close(Hd, H, rtol=1e-5, atol=1e-5)
