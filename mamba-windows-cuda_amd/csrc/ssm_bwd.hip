@@ -11,8 +11,9 @@
 //   dB     = sum_d g*delta*u                      dC = sum_d dout*h_t
 //   dh_prev = dA_0*g_0
 //
-// Mapping: the forward's lane groups (LPC lanes x SPL states per channel, 4
-// waves = CPB channels of one batch row per workgroup). The sequence is walked
+// Mapping: lane groups as in the forward (LPC lanes x SPL states per channel, 4
+// waves = CPB channels of one batch row per workgroup), but with the channel in
+// the low lane bits and the state group in the high ones. The sequence is walked
 // in reverse in chunks of 16 steps; each chunk restarts from the fp32
 // checkpoint the forward stored, recomputes the chunk's states and decay
 // factors into VGPRs (one exp per state) and runs the reverse sweep. Inputs
@@ -22,12 +23,13 @@
 // Sums over n (S1 = sum g*B and S2 = sum g*A*dA*h_{t-1}) are DPP reduce-scatters
 // inside the lane group; the storing threads finish du = D*dout + delta*S1 and
 // ddelta = S2 + u*S1 once per element. Sums over
-// channels (dB, dC) go through a wave-private LDS slab: each step the lanes
-// deposit g_t and h_t, and every 4 steps the wave folds its channels with one
-// FMA per state against the per-channel weights (delta*u for dB, dout for dC)
-// read from the staged tile; once per chunk the workgroup's waves are added and
-// written as a per-group fp32 partial, which a second small kernel sums in
-// fixed order (deterministic, no atomics). dA and dD accumulate in registers
+// channels (dB, dC) go through a wave-private LDS slab: each step a lane weights
+// g_t by delta*u and h_t by dout, adds its channel partner's weighted values
+// with one reduce-scatter level (keeping one of the two) and deposits the
+// result; every 4 steps the wave folds the deposited channel-pair columns. Once
+// per chunk the workgroup's waves are added and written as a per-group fp32
+// partial, which a second small kernel sums in fixed order (deterministic, no
+// atomics). dA and dD accumulate in registers
 // over t and are summed over the segments and b by the finishing kernel.
 //
 // Parallelism over L: as in the forward, L is cut into segments of whole
