@@ -15,8 +15,9 @@ struct SsmShape {
 #define MWC_FOR_EACH_LANE_GROUP(X) X(8, 1) X(8, 2) X(16, 1) X(16, 2) X(16, 4) X(32, 2) X(32, 4) X(64, 4)
 bool lane_group_supported(int ns, int spl);
 
-// Waves per SIMD the lane-group kernels are compiled to fit (each lane then has 512/W VGPRs).
-constexpr int fwd_min_waves(int spl) { return spl == 4 ? 1 : spl == 1 ? 6 : 3; }
+// Waves per SIMD the lane-group kernels are compiled to fit (each lane then has 512/W VGPRs). The
+// forward at four states per lane fits three waves without transforms and two with them.
+constexpr int fwd_min_waves(int spl) { return spl == 4 ? 2 : spl == 1 ? 6 : 3; }
 constexpr int bwd_min_waves(int spl) { return spl == 4 ? 1 : 3; }
 #ifndef MWC_CARRY_WAVES
 #define MWC_CARRY_WAVES 6

@@ -267,10 +267,10 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
         if (more) issue(k + 1);
         if (ckb != nullptr && valid) vst<SPL>(ckb + (int64_t)k * D * NS, h);
 
-        // the main pass reads the whole chunk's operands up front, so LDS latency is paid once per
-        // chunk; the state-only passes read them four steps at a time, which keeps them to few enough
-        // registers for twice the waves per SIMD (their chunks are short on arithmetic, so more waves
-        // in flight are what covers the loads)
+        // the main pass at two states per lane reads the whole chunk's operands up front, so LDS
+        // latency is paid once per chunk; the state-only passes read them four steps at a time, which
+        // keeps them to few enough registers for twice the waves per SIMD (their chunks are short on
+        // arithmetic, so more waves in flight are what covers the loads)
         float dt[TC], dtu[TC], Bv[TC][SPL], Cv[TC][SPL];
         auto read_steps = [&](int i0, int n) {
 #pragma unroll
@@ -299,8 +299,10 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
                 }
             }
         };
-        // the main pass at one state per lane runs many waves per SIMD too, and reads in groups as well
-        constexpr bool GROUPED = !HAS_OUT || SPL == 1;
+        // the main pass reads in groups as well at one state per lane (it runs many waves per SIMD
+        // too) and at four (reading the chunk up front would hold 160 VGPRs of operands: one wave per
+        // SIMD instead of three, and twice the time per call at N=64)
+        constexpr bool GROUPED = !HAS_OUT || SPL != 2;
         if constexpr (!GROUPED) read_steps(0, TC);
         // one workgroup-uniform decision per chunk: the loaders flag a chunk in which some |delta*A|
         // can exceed 88; the clamped path gives the same values whenever none does, so deciding for the
