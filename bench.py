@@ -429,6 +429,29 @@ def cpu_baseline(cfg, d_frac=2, runs=3):
                       f"affinity={cores}"}
 
 
+def cpu_baseline_pscan(runs=3):
+    """The reference's CPU path for cfg4b: parallel_scan_ref (pscan.py:153-171, the package's
+    restatement: one torch elementwise update per step over L), on the whole cfg4b workload in fp32;
+    the median of `runs` timed runs."""
+    import torch
+
+    from mamba_windows_cuda import parallel_scan_ref, workloads
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    a, b = workloads.pscan_inputs()
+    times = []
+    for _ in range(runs):
+        t = time.perf_counter()
+        parallel_scan_ref(a, b)
+        times.append(time.perf_counter() - t)
+    per = sorted(times)[len(times) // 2]
+    return {"value": a.numel() / per, "unit": "elements/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"cfg4b in full: parallel_scan_ref over {tuple(a.shape)} fp32 on the host; median of {runs} "
+                      f"runs ({', '.join(f'{t:.2f}' for t in times)} s); os.cpu_count()={os.cpu_count()}, "
+                      f"affinity={cores}"}
+
+
 def kernels_only(cfg):
     """Profiling driver: three fused forward/backward calls at `cfg`, three cfg4b scans and a
     1 GiB device copy (the copy calibrates rocprofv3's FETCH_SIZE/WRITE_SIZE counters)."""
@@ -462,7 +485,7 @@ TRACE_RUNS = {
     "cfg3_level0": ["--config", "cfg3", "--level", "0", "--skip-cpu", "--steps", "30"],
     "cfg3_level1": ["--config", "cfg3", "--level", "1", "--skip-cpu", "--steps", "30"],
     "cfg4a_stream": ["--config", "cfg4a", "--steps", "10"],
-    "cfg4b_pscan": ["--config", "cfg4b", "--steps", "50"],
+    "cfg4b_pscan": ["--config", "cfg4b", "--steps", "50", "--skip-cpu"],
     "decode_b1024": ["--decode", "1024", "--steps", "320"],
 }
 PMC_PASSES = {
@@ -693,6 +716,8 @@ def main():
                 "device": torch.cuda.get_device_name(0)})
     if not args.skip_cpu and args.config in ("cfg2", "cfg3"):
         res["cpu_baseline"] = cpu_baseline(args.config)
+    elif not args.skip_cpu and args.config == "cfg4b":
+        res["cpu_baseline"] = cpu_baseline_pscan()
     print(json.dumps(res))
 
 
