@@ -242,3 +242,45 @@ def test_selective_scan_backward_is_the_true_adjoint():
     inter.pop("A")
     with pytest.raises(RuntimeError, match="intermediates"):
         selective_scan_backward(dout, dhl, inter, Dv)
+
+
+def test_scan_status_queue_reports_finished_failures():
+    """The non-waiting scan status: words whose events have completed are retired in order, a non-zero
+    word raises MWC_ERR_INCOMPLETE, unfinished ones stay queued until pscan_check() waits for them."""
+    import torch
+
+    from mamba_windows_cuda import ops
+
+    class Ev:
+        def __init__(self, done):
+            self.done, self.waited = done, False
+
+        def query(self):
+            return self.done
+
+        def synchronize(self):
+            self.waited = True
+            self.done = True
+
+    q = ops._pending_status
+    saved = list(q)
+    q.clear()
+    try:
+        ok, bad, later = Ev(True), Ev(True), Ev(False)
+        q.extend([(ok, torch.zeros(1, dtype=torch.int32), "a"), (bad, torch.ones(1, dtype=torch.int32), "b"),
+                  (later, torch.zeros(1, dtype=torch.int32), "c")])
+        with pytest.raises(RuntimeError, match="b failed: MWC_ERR_INCOMPLETE"):
+            ops._drain_status()
+        assert [w for _, _, w in q] == ["c"] and not later.waited  # the unfinished one stays, not waited for
+        ops._drain_status()  # nothing finished: no error, still queued
+        assert len(q) == 1
+        ops.pscan_check()  # waits for it; its word is 0
+        assert later.waited and len(q) == 0
+        fail = Ev(False)
+        q.append((fail, torch.full((1,), 5, dtype=torch.int32), "d"))
+        with pytest.raises(RuntimeError, match="d failed"):
+            ops.pscan_check()
+        assert fail.waited and len(q) == 0
+    finally:
+        q.clear()
+        q.extend(saved)
