@@ -22,7 +22,7 @@ TOL = {torch.float32: dict(rtol=1e-3, atol=1e-4), torch.float16: dict(rtol=1e-2,
 GRADS = (("u", "du"), ("delta", "ddelta"), ("A", "dA"), ("B", "dB"), ("C", "dC"), ("D", "dD"))
 # states per lane built for each state count
 SPLS = {8: (1, 2), 16: (1, 2, 4), 32: (2, 4), 64: (4,)}
-NCASES = 40
+NCASES = 200
 
 
 def _case(idx):
