@@ -13,6 +13,7 @@ from __future__ import annotations
 import collections
 import functools
 import os
+import threading
 
 import torch
 
@@ -314,6 +315,7 @@ def _check_scan(*ts):
 # looks at the words whose events have completed. A bounded look-back wait that gave up (its tiles'
 # outputs are NaN) is so reported by the first scan call, or pscan_check(), after it finished.
 _pending_status = collections.deque()  # (event, pinned int32 word, what)
+_pending_lock = threading.Lock()
 _MAX_PENDING = 256
 
 
@@ -328,8 +330,10 @@ def _pscan_status(L_, ws, nbytes, nseq, L, nc, dev, what):
         _lib.check(st, what)
         ev = torch.cuda.Event()
         ev.record()
-    _pending_status.append((ev, word, what))
-    if len(_pending_status) > _MAX_PENDING:
+    with _pending_lock:
+        _pending_status.append((ev, word, what))
+        full = len(_pending_status) > _MAX_PENDING
+    if full:
         _drain_status(wait_oldest=True)
 
 
@@ -341,16 +345,17 @@ def _drain_status(wait_all=False, wait_oldest=False):
         return
     failed = None
     first = True
-    while _pending_status:
-        ev, word, what = _pending_status[0]
-        if wait_all or (wait_oldest and first):
-            ev.synchronize()
-        elif not ev.query():
-            break
-        first = False
-        _pending_status.popleft()
-        if int(word[0]) != 0 and failed is None:
-            failed = what
+    with _pending_lock:
+        while _pending_status:
+            ev, word, what = _pending_status[0]
+            if wait_all or (wait_oldest and first):
+                ev.synchronize()
+            elif not ev.query():
+                break
+            first = False
+            _pending_status.popleft()
+            if int(word[0]) != 0 and failed is None:
+                failed = what
     if failed is not None:
         raise RuntimeError(f"{failed} failed: MWC_ERR_INCOMPLETE: a look-back wait of an earlier parallel scan "
                            "ran out of spins, so the affected tiles' outputs are NaN")
