@@ -92,10 +92,14 @@ int env_int(const char* name, int lo, int hi) {
     return (v >= lo && v <= hi) ? v : 0;
 }
 
-// Relative throughput of a SIMD running q of these (issue- and latency-bound) waves at once
-// (measured on the config-2 / config-3 kernels: a second wave doubles it, a third adds ~8%).
+// Relative throughput of a SIMD running q of these waves at once. Measured with the main kernels at
+// 2 states per lane, B=8, L=2048, one segment and D = 1024, 2048, 3072 (1, 2, 3 workgroups per CU):
+// 1 : 1.65-1.7 : 2.0 for the forward and the backward. The table takes 1.55 for two waves: a last round
+// of two waves per SIMD that starts while the previous round drains runs below the steady rate
+// (config 3: one backward segment at 2.5 workgroups per CU beat two segments by 6%). Four or more
+// waves (the carry passes, one state per lane) keep the earlier estimates.
 double simd_throughput(int64_t q) {
-    static const double t[] = {0.0, 1.0, 2.0, 2.15, 2.3};
+    static const double t[] = {0.0, 1.0, 1.55, 2.0, 2.3};
     return q < 5 ? t[q] : 2.4;
 }
 
