@@ -94,20 +94,17 @@ int env_int(const char* name, int lo, int hi) {
 
 // Relative throughput of a SIMD running q of these waves at once. Measured with the main kernels at
 // 2 states per lane, B=8, L=2048, one segment and D = 1024, 2048, 3072 (1, 2, 3 workgroups per CU):
-// 1 : 1.65-1.7 : 2.0 for the forward and the backward. The table takes 1.55 for two waves: a last round
-// of two waves per SIMD that starts while the previous round drains runs below the steady rate
-// (config 3: one backward segment at 2.5 workgroups per CU beat two segments by 6%). Four or more
-// waves (the carry passes, one state per lane) keep the earlier estimates.
+// 1 : 1.65-1.7 : 2.0 for the forward and the backward. Four or more waves (the carry passes, one
+// state per lane) keep earlier estimates.
 double simd_throughput(int64_t q) {
-    static const double t[] = {0.0, 1.0, 1.55, 2.0, 2.3};
+    static const double t[] = {0.0, 1.0, 1.7, 2.0, 2.3};
     return q < 5 ? t[q] : 2.4;
 }
 
 // Duration, in units of one chunk of one lone wave, of a pass of `wgs` equal workgroups of
 // `chunks` chunks each when a CU holds at most `cap` of them at once: full rounds of `cap`, then
-// a last round as deep as its busiest CU. Grids of more than one round run a little faster per
-// round than one lock-step round (measured): workgroups that start at different times overlap
-// their LDS-heavy and VALU-heavy phases.
+// a last round as deep as its busiest CU. (Counting the rounds one after the other matches the
+// measured plans; an earlier 4% discount for grids of several rounds overrated split plans.)
 double pass_time(int64_t wgs, int64_t chunks, int cap) {
     if (wgs <= 0 || chunks <= 0) return 0.0;
     const int64_t full = wgs / (kCUs * cap);
@@ -117,7 +114,7 @@ double pass_time(int64_t wgs, int64_t chunks, int cap) {
         const int64_t q = (rem + kCUs - 1) / kCUs;
         t += (double)chunks * q / simd_throughput(q) + 1.0;
     }
-    return full + (rem > 0 ? 1 : 0) > 1 ? 0.96 * t : t;
+    return t;
 }
 
 int cpb_of(int ns, int spl) { return 4 * 64 / (ns / spl); }
