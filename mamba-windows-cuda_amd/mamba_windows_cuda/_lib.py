@@ -63,6 +63,10 @@ _SIGNATURES = {
 EXPORTED = tuple(_SIGNATURES)
 
 
+TORCH_OPS_PATH = os.path.join(_HERE, "libmwc_torch.so")
+_torch_ops = None
+
+
 class NativeLibraryMissing(ImportError):
     pass
 
@@ -85,6 +89,25 @@ def lib():
                 fn.restype = res
             _lib = handle
     return _lib
+
+
+def torch_ops():
+    """Load (once) libmwc_torch.so, the PyTorch operators over the C ABI (csrc/torch_ops.cpp), and
+    return their namespace, ``torch.ops.mwc``; raises if it is not built."""
+    global _torch_ops
+    if _torch_ops is not None:
+        return _torch_ops
+    with _lock:
+        if _torch_ops is None:
+            if not os.path.exists(TORCH_OPS_PATH):
+                raise NativeLibraryMissing(
+                    f"{TORCH_OPS_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'` "
+                    "or `make -C mamba-windows-cuda_amd/csrc`")
+            import torch
+
+            torch.ops.load_library(TORCH_OPS_PATH)
+            _torch_ops = torch.ops.mwc
+    return _torch_ops
 
 
 def check(status: int, what: str) -> None:

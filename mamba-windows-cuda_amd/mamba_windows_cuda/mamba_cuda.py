@@ -24,7 +24,19 @@ from __future__ import annotations
 
 import torch
 
-from . import ops
+from . import _lib, ops
+
+_scan_op = None
+
+
+def _ssm_scan(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, checkpoint_lvl, z, delta_bias, delta_softplus):
+    """(out, h_last) through ``torch.ops.mwc.ssm_scan`` (csrc/torch_ops.cpp): the same checks,
+    kernels and gradients as SelectiveScanCudaFunction, with the argument checks, allocation,
+    launch and autograd Function in C++ rather than Python."""
+    global _scan_op
+    if _scan_op is None:
+        _scan_op = _lib.torch_ops().ssm_scan.default
+    return _scan_op(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, checkpoint_lvl, z, delta_bias, bool(delta_softplus))
 
 
 def _forward_impl(ctx, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, checkpoint_lvl, z=None, delta_bias=None,
@@ -65,7 +77,10 @@ class SelectiveScanCudaFunction(torch.autograd.Function):
     """(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, checkpoint_lvl=0, z=None, delta_bias=None,
     delta_softplus=False) -> (out, h_last); backward returns dh_prev when h_prev is given
     (mamba_cuda.py:1044-1096). The last three arguments are the fused transforms (delta' =
-    softplus(delta + delta_bias), out = scan * silu(z)); the reference has no counterpart."""
+    softplus(delta + delta_bias), out = scan * silu(z)); the reference has no counterpart.
+    This is the Python host path (ops.py over ctypes); SelectiveScanCuda and FusedSelectiveScan
+    call the C++ operator ``torch.ops.mwc.ssm_scan``, which runs the same kernels with the same
+    checks and gives bitwise the same results with less host time per call."""
 
     @staticmethod
     def forward(ctx, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, checkpoint_lvl=0, z=None, delta_bias=None,
@@ -114,7 +129,9 @@ class SelectiveScanCuda(torch.nn.Module):
     N = 16 as in the reference, or 8, 32, 64. All tensors fp32 or all fp16 (or
     all bf16), on the GPU; outputs and gradients take the
     input dtype. ``checkpoint_lvl`` (keyword, default 0) picks the memory/speed
-    trade-off described in the module docstring.
+    trade-off described in the module docstring. The calls go through the C++ operator
+    ``torch.ops.mwc.ssm_scan`` (argument checks, allocation, launch and the autograd Function
+    in C++).
 
     Keyword-only extras fused into the kernels (not in the reference; the
     options a Mamba block applies around the scan): ``delta_bias`` (D,) and
@@ -129,15 +146,14 @@ class SelectiveScanCuda(torch.nn.Module):
 
     def forward(self, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, *, z=None, delta_bias=None,
                 delta_softplus=False):
-        out, _ = SelectiveScanCudaFunction.apply(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, self.checkpoint_lvl, z,
-                                                 delta_bias, delta_softplus)
-        return out
+        return _ssm_scan(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, self.checkpoint_lvl, z, delta_bias,
+                         delta_softplus)[0]
 
     def forward_with_state(self, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, *, z=None, delta_bias=None,
                            delta_softplus=False):
         """Returns (out (B, L, D), h_last (B, D, N)); h_last feeds the next chunk's h_prev."""
-        return SelectiveScanCudaFunction.apply(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, self.checkpoint_lvl, z,
-                                               delta_bias, delta_softplus)
+        return _ssm_scan(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, self.checkpoint_lvl, z, delta_bias,
+                         delta_softplus)
 
     def step(self, u, delta, A, B_ssm, C_ssm, D_ssm, h, *, z=None, delta_bias=None, delta_softplus=False,
              out_state=None):

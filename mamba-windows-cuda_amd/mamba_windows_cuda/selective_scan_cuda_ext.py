@@ -13,11 +13,12 @@ from __future__ import annotations
 
 import torch
 
-from .mamba_cuda import _backward_impl, _forward_impl
+from .mamba_cuda import _backward_impl, _forward_impl, _ssm_scan
 
 
 class FusedSelectiveScanFunction(torch.autograd.Function):
-    """(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, checkpoint_lvl=0) -> (out, h_last)."""
+    """(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, checkpoint_lvl=0) -> (out, h_last), on the
+    Python host path; FusedSelectiveScan calls the C++ operator torch.ops.mwc.ssm_scan instead."""
 
     @staticmethod
     def forward(ctx, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, checkpoint_lvl=0):
@@ -38,8 +39,7 @@ class FusedSelectiveScan(torch.nn.Module):
         self.checkpoint_lvl = checkpoint_lvl
 
     def forward(self, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None):
-        out, _ = FusedSelectiveScanFunction.apply(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, self.checkpoint_lvl)
-        return out
+        return _ssm_scan(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, self.checkpoint_lvl, None, None, False)[0]
 
     def forward_with_state(self, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None):
-        return FusedSelectiveScanFunction.apply(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, self.checkpoint_lvl)
+        return _ssm_scan(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, self.checkpoint_lvl, None, None, False)

@@ -27,6 +27,27 @@ def test_library_exports_every_declared_symbol():
     assert L.mwc_abi_version() == 1
 
 
+def test_torch_operator_library_registers_ssm_scan():
+    """libmwc_torch.so (the C++ host path) loads and registers torch.ops.mwc.ssm_scan with the
+    reference's argument names; host tensors are refused by its checks in every dispatch mode."""
+    from mamba_windows_cuda import _lib
+
+    ops = _lib.torch_ops()
+    schema = str(ops.ssm_scan.default._schema)
+    for arg in ("Tensor u", "Tensor delta", "Tensor A", "Tensor B_ssm", "Tensor C_ssm", "Tensor D_ssm",
+                "Tensor? h_prev=None", "int checkpoint_lvl=0", "Tensor? z=None", "Tensor? delta_bias=None",
+                "bool delta_softplus=False"):
+        assert arg in schema, arg
+    x = _valid()
+    args = [x["u"], x["delta"], x["A"], x["B_ssm"], x["C_ssm"], x["D_ssm"]]
+    with pytest.raises(RuntimeError, match="u must be a CUDA tensor"):
+        ops.ssm_scan(*args)
+    with pytest.raises(RuntimeError, match="u must be a CUDA tensor"):
+        ops.ssm_scan(*[t.clone().requires_grad_(True) for t in args])
+    with torch.inference_mode(), pytest.raises(RuntimeError, match="u must be a CUDA tensor"):
+        ops.ssm_scan(*args)
+
+
 def test_status_strings_and_ckpt_count():
     from mamba_windows_cuda import _lib
 

@@ -1,0 +1,121 @@
+"""The C++ host path (torch.ops.mwc.ssm_scan, csrc/torch_ops.cpp), which SelectiveScanCuda and
+FusedSelectiveScan call, against the Python host path (SelectiveScanCudaFunction over ops.py and
+ctypes): both enqueue the same kernels with the same launch plans, so out, h_last and every gradient
+must agree bitwise, for every combination of h_prev, the fused transforms, checkpoint level and
+storage dtype. Also: the argument checks give the reference's messages on device tensors, and a call
+that needs no gradient keeps nothing."""
+import pytest
+import torch
+
+from mamba_windows_cuda import SelectiveScanCuda, workloads
+from mamba_windows_cuda.mamba_cuda import SelectiveScanCudaFunction, _ssm_scan
+
+pytestmark = pytest.mark.gpu
+
+NAMES = ("u", "delta", "A", "B", "C", "D")
+
+
+def _leaves(x, dev, keys):
+    return {k: x[k].to(dev).requires_grad_(True) for k in keys}
+
+
+def _step(fn, x, dev, *, with_h, gated, biased, softplus, lvl, dh_last):
+    keys = NAMES + (("h_prev",) if with_h else ())
+    lv = _leaves(x, dev, keys)
+    extra = {}
+    if gated:
+        extra["z"] = x["z"].to(dev).requires_grad_(True)
+    if biased:
+        extra["delta_bias"] = x["delta_bias"].to(dev).requires_grad_(True)
+    out, h_last = fn(*(lv[k] for k in NAMES), lv.get("h_prev"), lvl, extra.get("z"), extra.get("delta_bias"),
+                     softplus)
+    loss = (out.float() * x["dout"].to(dev).float()).sum()
+    if dh_last:
+        loss = loss + (h_last.float() * x["dh_last"].to(dev).float()).sum()
+    loss.backward()
+    torch.cuda.synchronize()
+    grads = {k: t.grad for k, t in {**lv, **extra}.items()}
+    return out.detach(), h_last.detach(), grads
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16], ids=["f32", "f16", "bf16"])
+@pytest.mark.parametrize("with_h,gated,biased,softplus,lvl,dh_last", [
+    (False, False, False, False, 0, False),
+    (True, False, False, False, 0, True),
+    (True, False, False, False, 1, True),
+    (False, True, True, True, 0, False),
+    (True, True, True, True, 1, True),
+    (False, False, True, False, 1, False),
+], ids=["plain", "h_prev", "h_prev_lvl1", "xf", "xf_h_lvl1", "bias_lvl1"])
+def test_cpp_path_equals_python_path_bitwise(dev, dtype, with_h, gated, biased, softplus, lvl, dh_last):
+    print(f"case torch op vs python {dtype} h={with_h} z={gated} bias={biased} sp={softplus} lvl={lvl}",
+          flush=True)
+    B, L, D = 2, 300, 96
+    x = workloads.ssm_inputs(B, L, D, dtype=dtype, h_prev=True, seed=17)
+    g = torch.Generator().manual_seed(5)
+    x["z"] = torch.randn(B, L, D, generator=g).to(dtype)
+    x["delta_bias"] = (0.1 * torch.randn(D, generator=g)).to(dtype)
+    x["dh_last"] = torch.randn(B, D, 16, generator=g).to(dtype)
+    kw = dict(with_h=with_h, gated=gated, biased=biased, softplus=softplus, lvl=lvl, dh_last=dh_last)
+    o1, h1, g1 = _step(_ssm_scan, x, dev, **kw)
+    o2, h2, g2 = _step(SelectiveScanCudaFunction.apply, x, dev, **kw)
+    assert torch.equal(o1, o2) and torch.equal(h1, h2)
+    assert g1.keys() == g2.keys()
+    for k in g1:
+        assert g1[k] is not None and torch.equal(g1[k], g2[k]), k
+
+
+@pytest.mark.parametrize("mutate,msg", [
+    (lambda x: x.update(A=torch.randn(3, 15)), "Only N=16"),
+    (lambda x: x.update(A=torch.randn(3, 32)), "B_ssm shape mismatch"),
+    (lambda x: x.update(u=x["u"].double()), "float32/float16"),
+    (lambda x: x.update(delta=x["delta"].half()), "delta dtype must match"),
+    (lambda x: x.update(u=x["u"][0]), "u must be 3D"),
+    (lambda x: x.update(B=torch.randn(2, 4, 16)), "B_ssm shape mismatch"),
+    (lambda x: x.update(D=torch.ones(4)), "D_ssm shape mismatch"),
+    (lambda x: x.update(C=torch.randn(2, 16, 5).transpose(1, 2)), "C_ssm must be contiguous"),
+    (lambda x: x.update(h_prev=torch.randn(2, 3, 17)), "h_prev shape must be"),
+    (lambda x: x.update(h_prev=torch.randn(3, 3, 16)), "h_prev shape must be"),
+    (lambda x: x.update(h_prev=torch.randn(2, 3, 16).half()), "h_prev dtype"),
+    (lambda x: x.update(z=torch.randn(2, 5, 4)), r"z shape must be \(2, 5, 3\)"),
+    (lambda x: x.update(delta_bias=torch.randn(4)), r"delta_bias shape must be \(3,\)"),
+    (lambda x: x.update(lvl=2), "checkpoint_lvl must be 0 or 1"),
+])
+def test_operator_argument_checks(dev, mutate, msg):
+    """The reference's TORCH_CHECK contract (mamba_cuda.py:281-326) on device tensors, raised before any
+    work is queued."""
+    x = dict(u=torch.randn(2, 5, 3), delta=torch.rand(2, 5, 3), A=-torch.rand(3, 16), B=torch.randn(2, 5, 16),
+             C=torch.randn(2, 5, 16), D=torch.ones(3), h_prev=None, z=None, delta_bias=None, lvl=0)
+    mutate(x)
+    d = {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in x.items()}
+    with pytest.raises(RuntimeError, match=msg):
+        _ssm_scan(d["u"], d["delta"], d["A"], d["B"], d["C"], d["D"], d["h_prev"], d["lvl"], d["z"],
+                  d["delta_bias"], False)
+
+
+def test_operator_without_gradients_keeps_nothing(dev):
+    x = {k: v.to(dev) for k, v in workloads.ssm_inputs(1, 100, 64, seed=3).items()}
+    m = SelectiveScanCuda()
+    ref = m(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"])
+    assert ref.grad_fn is None
+    with torch.inference_mode():
+        out = m(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"])
+    lv = {k: x[k].clone().requires_grad_(True) for k in NAMES}
+    with torch.no_grad():
+        out2 = m(*(lv[k] for k in NAMES))
+    assert out2.grad_fn is None
+    assert torch.equal(out, ref) and torch.equal(out2, ref)
+
+
+def test_operator_gradient_from_h_last_only(dev):
+    """A loss on h_last alone gives no dout: the backward treats it as zeros (and vice versa)."""
+    x = workloads.ssm_inputs(2, 70, 40, h_prev=True, seed=9)
+    res = []
+    for fn in (_ssm_scan, SelectiveScanCudaFunction.apply):
+        lv = {k: x[k].to(dev).requires_grad_(True) for k in NAMES + ("h_prev",)}
+        out, h_last = fn(*(lv[k] for k in NAMES), lv["h_prev"], 0, None, None, False)
+        h_last.sum().backward()
+        torch.cuda.synchronize()
+        res.append({k: t.grad for k, t in lv.items()})
+    for k in res[0]:
+        assert torch.equal(res[0][k], res[1][k]), k
