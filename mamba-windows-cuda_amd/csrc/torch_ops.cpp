@@ -7,6 +7,8 @@
 //
 //   torch.ops.mwc.ssm_scan(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, checkpoint_lvl=0,
 //                          z=None, delta_bias=None, delta_softplus=False) -> (out, h_last)
+//   torch.ops.mwc.ssm_step(u, delta, A, B_ssm, C_ssm, D_ssm, h, z=None, delta_bias=None,
+//                          delta_softplus=False, out_state=None) -> (out, h_new)   (decode, inference)
 //
 // checkpoint_lvl 0 keeps the forward's fp32 state checkpoints (every 16 steps) for the backward; 1
 // keeps only the inputs and rebuilds them with a state-only forward pass in the backward. Nothing
@@ -267,14 +269,89 @@ std::tuple<Tensor, Tensor> scan_autograd(const Tensor& u, const Tensor& delta, c
     return {r[0], r[1]};
 }
 
+// One decode step (as ops.ssm_step): u, delta, z (B, D); A (D, N); B_ssm, C_ssm (B, N); D_ssm (D,);
+// h (B, D, N). Returns (out (B, D), gated by silu(z) when z is given, h_new); out_state, when given,
+// receives h_new and may be h itself (an in-place update). Inference only.
+std::tuple<Tensor, Tensor> step_impl(const Tensor& u_, const Tensor& delta_, const Tensor& A_, const Tensor& B_,
+                                     const Tensor& C_, const Tensor& D_, const Tensor& h_, const OptT& z_,
+                                     const OptT& delta_bias_, bool softplus, const OptT& out_state) {
+    const std::pair<const char*, const Tensor*> named[] = {{"u", &u_}, {"delta", &delta_}, {"A", &A_}, {"B_ssm", &B_},
+                                                           {"C_ssm", &C_}, {"D_ssm", &D_}, {"h", &h_}};
+    for (const auto& [name, t] : named) {
+        TORCH_CHECK(t->is_cuda(), name, " must be a CUDA tensor");
+        TORCH_CHECK(t->scalar_type() == u_.scalar_type(), name, " dtype must match u dtype");
+    }
+    const auto dt = u_.scalar_type();
+    TORCH_CHECK(dt == at::kFloat || dt == at::kHalf || dt == at::kBFloat16, "u must be float32/float16 (or bfloat16)");
+    TORCH_CHECK(u_.dim() == 2, "u must be 2D (batch, dim) for a step");
+    const int64_t bsz = u_.size(0), dm = u_.size(1);
+    TORCH_CHECK(A_.dim() == 2 && (A_.size(1) == 8 || A_.size(1) == 16 || A_.size(1) == 32 || A_.size(1) == 64),
+                "Only N=16 (or 8, 32, 64) is supported");
+    const int64_t n = A_.size(1);
+    const std::tuple<const char*, const Tensor*, std::vector<int64_t>> shaped[] = {
+        {"delta", &delta_, {bsz, dm}}, {"A", &A_, {dm, n}}, {"B_ssm", &B_, {bsz, n}}, {"C_ssm", &C_, {bsz, n}},
+        {"D_ssm", &D_, {dm}}, {"h", &h_, {bsz, dm, n}},
+        {"delta_bias", delta_bias_.has_value() ? &*delta_bias_ : nullptr, {dm}},
+        {"z", z_.has_value() ? &*z_ : nullptr, {bsz, dm}}};
+    for (const auto& [name, t, shape] : shaped) {
+        if (t == nullptr) continue;
+        TORCH_CHECK(t->sizes() == at::IntArrayRef(shape), name, " shape must be ", shape_str(shape));
+        TORCH_CHECK(t->scalar_type() == dt && t->device() == u_.device(), name, " must match u's dtype and device");
+    }
+    // the kernel moves a lane's states as one 16-byte vector
+    auto aligned = [](const Tensor& t) {
+        Tensor c = t.contiguous();
+        return reinterpret_cast<uintptr_t>(c.data_ptr()) % 16 == 0 ? c : c.clone();
+    };
+    const Tensor u = u_.contiguous(), delta = delta_.contiguous(), D = D_.contiguous();
+    const Tensor A = aligned(A_), B = aligned(B_), C = aligned(C_), h = aligned(h_);
+    const Tensor delta_bias = contig(delta_bias_), z = contig(z_);
+    Tensor h_new = out_state.has_value() ? *out_state : at::empty_like(h);
+    TORCH_CHECK(h_new.is_contiguous() && h_new.dim() == 3 && h_new.size(0) == bsz && h_new.size(1) == dm &&
+                    h_new.size(2) == n && h_new.scalar_type() == dt &&
+                    reinterpret_cast<uintptr_t>(h_new.data_ptr()) % 16 == 0,
+                "out_state must be a contiguous, 16-byte-aligned (B, D, N) tensor of u's dtype");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(u.device());
+    const Tensor out = at::empty_like(u);
+    check_status(mwc_ssm_step(dtype_code(u), ptr(u), ptr(delta), ptr(A), ptr(B), ptr(C), ptr(D), ptr(h),
+                              ptr(delta_bias), softplus ? 1 : 0, ptr(z), z.defined() ? nullptr : ptr(out),
+                              z.defined() ? ptr(out) : nullptr, ptr(h_new), bsz, dm, n, stream_of(u)),
+                 "mwc_ssm_step");
+    return {out, h_new};
+}
+
+std::tuple<Tensor, Tensor> step_autograd(const Tensor& u, const Tensor& delta, const Tensor& A, const Tensor& B,
+                                         const Tensor& C, const Tensor& D, const Tensor& h, const OptT& z,
+                                         const OptT& delta_bias, bool softplus, const OptT& out_state) {
+    if (at::GradMode::is_enabled()) {
+        bool req = false;
+        for (const Tensor* t : {&u, &delta, &A, &B, &C, &D, &h}) req = req || t->requires_grad();
+        for (const OptT* t : {&z, &delta_bias}) req = req || (t->has_value() && (*t)->requires_grad());
+        TORCH_CHECK(!req, "SelectiveScanCuda.step is inference-only; use forward_with_state for gradients");
+    }
+    return step_impl(u, delta, A, B, C, D, h, z, delta_bias, softplus, out_state);
+}
+
 }  // namespace
 
 TORCH_LIBRARY(mwc, m) {
     m.def("ssm_scan(Tensor u, Tensor delta, Tensor A, Tensor B_ssm, Tensor C_ssm, Tensor D_ssm, Tensor? h_prev=None, "
           "int checkpoint_lvl=0, Tensor? z=None, Tensor? delta_bias=None, bool delta_softplus=False) -> (Tensor, Tensor)");
+    m.def("ssm_step(Tensor u, Tensor delta, Tensor A, Tensor B_ssm, Tensor C_ssm, Tensor D_ssm, Tensor h, "
+          "Tensor? z=None, Tensor? delta_bias=None, bool delta_softplus=False, Tensor(a!)? out_state=None) "
+          "-> (Tensor, Tensor)");
 }
 
-TORCH_LIBRARY_IMPL(mwc, Autograd, m) { m.impl("ssm_scan", &scan_autograd); }
+TORCH_LIBRARY_IMPL(mwc, Autograd, m) {
+    m.impl("ssm_scan", &scan_autograd);
+    m.impl("ssm_step", &step_autograd);
+}
 // HIP tensors carry torch's CUDA dispatch key; host tensors reach the same checks and are refused.
-TORCH_LIBRARY_IMPL(mwc, CUDA, m) { m.impl("ssm_scan", &scan_nograd); }
-TORCH_LIBRARY_IMPL(mwc, CPU, m) { m.impl("ssm_scan", &scan_nograd); }
+TORCH_LIBRARY_IMPL(mwc, CUDA, m) {
+    m.impl("ssm_scan", &scan_nograd);
+    m.impl("ssm_step", &step_impl);
+}
+TORCH_LIBRARY_IMPL(mwc, CPU, m) {
+    m.impl("ssm_scan", &scan_nograd);
+    m.impl("ssm_step", &step_impl);
+}

@@ -27,6 +27,7 @@ import torch
 from . import _lib, ops
 
 _scan_op = None
+_step_op = None  # torch.ops.mwc.ssm_step: the decode step's checks and launch in C++ (as ops.ssm_step)
 
 
 def _ssm_scan(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, checkpoint_lvl, z, delta_bias, delta_softplus):
@@ -160,11 +161,10 @@ class SelectiveScanCuda(torch.nn.Module):
         """One decode step (inference only; not in the reference, whose way to advance one token is
         forward_with_state with L=1). u, delta, z: (B, D); B_ssm, C_ssm: (B, N); h: (B, D, N).
         Returns (out (B, D), h_new (B, D, N)); pass out_state=h to update the state in place."""
-        if torch.is_grad_enabled() and any(t is not None and t.requires_grad
-                                           for t in (u, delta, A, B_ssm, C_ssm, D_ssm, h, z, delta_bias)):
-            raise RuntimeError("SelectiveScanCuda.step is inference-only; use forward_with_state for gradients")
-        return ops.ssm_step(u, delta, A, B_ssm, C_ssm, D_ssm, h, delta_bias=delta_bias,
-                            delta_softplus=delta_softplus, z=z, out_state=out_state)
+        global _step_op
+        if _step_op is None:
+            _step_op = _lib.torch_ops().ssm_step.default
+        return _step_op(u, delta, A, B_ssm, C_ssm, D_ssm, h, z, delta_bias, bool(delta_softplus), out_state)
 
 
 def selective_scan_ref(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, return_intermediates=False):

@@ -46,6 +46,10 @@ def test_torch_operator_library_registers_ssm_scan():
         ops.ssm_scan(*[t.clone().requires_grad_(True) for t in args])
     with torch.inference_mode(), pytest.raises(RuntimeError, match="u must be a CUDA tensor"):
         ops.ssm_scan(*args)
+    assert "Tensor(a!)? out_state=None" in str(ops.ssm_step.default._schema)
+    with pytest.raises(RuntimeError, match="u must be a CUDA tensor"):
+        ops.ssm_step(x["u"][:, 0], x["delta"][:, 0], x["A"], x["B_ssm"][:, 0], x["C_ssm"][:, 0], x["D_ssm"],
+                     torch.zeros(2, 3, 16))
 
 
 def test_status_strings_and_ckpt_count():

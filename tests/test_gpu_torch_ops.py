@@ -119,3 +119,40 @@ def test_operator_gradient_from_h_last_only(dev):
         res.append({k: t.grad for k, t in lv.items()})
     for k in res[0]:
         assert torch.equal(res[0][k], res[1][k]), k
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16], ids=["f32", "f16", "bf16"])
+@pytest.mark.parametrize("xf", [False, True], ids=["plain", "xf"])
+def test_step_operator_equals_python_step(dev, dtype, xf):
+    """SelectiveScanCuda.step (torch.ops.mwc.ssm_step) against ops.ssm_step: out and h_new bitwise, out of
+    place and in place, and with A / h that are not 16-byte aligned (both paths copy them first)."""
+    from mamba_windows_cuda import ops
+
+    print(f"case step operator vs python {dtype} xf={xf}", flush=True)
+    Bsz, D, N = 5, 200, 16
+    x = workloads.ssm_inputs(Bsz, 1, D, dtype=dtype, h_prev=True, seed=23)
+    g = torch.Generator().manual_seed(2)
+    kw = {}
+    if xf:
+        kw = dict(z=torch.randn(Bsz, D, generator=g).to(dtype).to(dev),
+                  delta_bias=(0.1 * torch.randn(D, generator=g)).to(dtype).to(dev), delta_softplus=True)
+    args = [x["u"][:, 0].to(dev), x["delta"][:, 0].to(dev), x["A"].to(dev), x["B"][:, 0].to(dev),
+            x["C"][:, 0].to(dev), x["D"].to(dev)]
+    h = x["h_prev"].to(dev)
+    m = SelectiveScanCuda()
+    y1, h1 = m.step(*args, h, **kw)
+    y2, h2 = ops.ssm_step(*args, h, **kw)
+    assert torch.equal(y1, y2) and torch.equal(h1, h2)
+    hc = h.clone()
+    y3, h3 = m.step(*args, hc, out_state=hc, **kw)
+    assert h3.data_ptr() == hc.data_ptr() and torch.equal(y3, y1) and torch.equal(hc, h1)
+    # misaligned A and h: views one element into a larger buffer
+    A_buf = torch.empty(D * N + 1, dtype=dtype, device=dev)
+    A_mis = A_buf[1:].view(D, N)
+    A_mis.copy_(args[2])
+    h_buf = torch.empty(Bsz * D * N + 1, dtype=dtype, device=dev)
+    h_mis = h_buf[1:].view(Bsz, D, N)
+    h_mis.copy_(h)
+    y4, h4 = m.step(args[0], args[1], A_mis, *args[3:], h_mis, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(y4, y1) and torch.equal(h4, h1)
