@@ -649,6 +649,106 @@ def summarize(out, dest=None):
     return written
 
 
+# The reference's own benchmark procedures (benchmark.py:26-253): the same shapes, input distributions,
+# warm-up and iteration counts and wall-clock timing around torch.cuda.synchronize(). Its published
+# figures (NVIDIA RTX 5070 Laptop GPU, BENCHMARK_RESULTS.md:12-34) are printed beside these for
+# context only: other hardware, and its "Fused" columns come from an extension that does not build.
+REF_FWD_MS = {(1, 512, 256): (2.50, 1.80), (1, 1024, 256): (5.10, 3.40), (1, 2048, 512): (15.20, 9.80),
+              (1, 4096, 768): (45.30, 28.50), (1, 8192, 1024): (120.50, 72.30), (1, 16384, 2048): (350.20, 195.80)}
+REF_TRAIN_MS = {(1, 512, 256): (8.50, 5.20, 6.10), (1, 1024, 256): (18.20, 10.50, 12.80),
+                (1, 2048, 512): (55.80, 30.20, 38.50), (1, 4096, 768): (165.50, 85.20, 110.50)}
+REF_MEM_MB = {"Original": (245.3, 892.1), "Fused(ckpt0)": (198.5, 756.2), "Fused(ckpt1)": (152.8, 523.4)}
+
+
+def reference_suite():
+    """benchmark_forward_only / benchmark_forward_backward / benchmark_memory of the reference, run
+    through this package: "Original" is SelectiveScanCuda, "Fused(ckpt0/1)" FusedSelectiveScan."""
+    import torch
+
+    from mamba_windows_cuda import FusedSelectiveScan, SelectiveScanCuda
+
+    dev, N = "cuda", 16
+    torch.manual_seed(0)
+    orig, fused0, fused1 = SelectiveScanCuda(), FusedSelectiveScan(0), FusedSelectiveScan(1)
+
+    def wall_ms(fn, n):
+        torch.cuda.synchronize()
+        t = time.time()
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        return (time.time() - t) / n * 1e3
+
+    res = {"suite": "the reference's benchmark.py procedures (wall clock, synchronize)", "forward_fp16": [],
+           "train_fp32": [], "memory_fp32_B1_L4096_D768": []}
+    _ref_forward(res, orig, fused0, wall_ms, dev, N)
+    _ref_train(res, orig, fused0, fused1, wall_ms, dev, N)
+    _ref_memory(res, orig, fused0, fused1, dev, N)
+    return res
+
+
+def _ref_train_inputs(B, L, D, dev, N):
+    import torch
+
+    return [torch.randn(B, L, D, device=dev), torch.ones(B, L, D, device=dev) * 0.01,
+            -torch.rand(D, N, device=dev) * 0.1, torch.randn(B, L, N, device=dev) * 0.1,
+            torch.randn(B, L, N, device=dev) * 0.1, torch.ones(D, device=dev) * 0.1]
+
+
+# (each section in a function of its own, so that its tensors are freed before the next one runs)
+def _ref_forward(res, orig, fused0, wall_ms, dev, N):
+    import torch
+
+    for (B, L, D), ref in REF_FWD_MS.items():
+        x = (torch.randn(B, L, D, device=dev).half(), torch.ones(B, L, D, device=dev).half(),
+             (-torch.rand(D, N, device=dev) * 0.1).half(), torch.randn(B, L, N, device=dev).half(),
+             torch.randn(B, L, N, device=dev).half(), torch.ones(D, device=dev).half())
+        for _ in range(5):
+            orig(*x)
+            fused0(*x)
+        t_o, t_f = wall_ms(lambda: orig(*x), 50), wall_ms(lambda: fused0(*x), 50)
+        res["forward_fp16"].append({"B": B, "L": L, "D": D, "original_ms": t_o, "fused_ms": t_f,
+                                    "reference_rtx5070_original_fused_ms": ref})
+
+
+def _ref_train(res, orig, fused0, fused1, wall_ms, dev, N):
+    for (B, L, D), ref in REF_TRAIN_MS.items():
+        base = _ref_train_inputs(B, L, D, dev, N)
+        row = {"B": B, "L": L, "D": D}
+        for name, k in (("original_ms", orig), ("fused_ckpt0_ms", fused0), ("fused_ckpt1_ms", fused1)):
+            leaves = [t.clone().requires_grad_(True) for t in base]
+
+            def step():
+                for t in leaves:
+                    t.grad = None
+                out, h = k.forward_with_state(*leaves)
+                (out.sum() + h.sum()).backward()
+
+            for _ in range(3):
+                step()
+            row[name] = wall_ms(step, 20)
+        row["reference_rtx5070_original_ckpt0_ckpt1_ms"] = ref
+        res["train_fp32"].append(row)
+
+
+def _ref_memory(res, orig, fused0, fused1, dev, N):
+    import torch
+
+    for name, k in (("Original", orig), ("Fused(ckpt0)", fused0), ("Fused(ckpt1)", fused1)):
+        torch.cuda.reset_peak_memory_stats()
+        torch.cuda.empty_cache()
+        x = _ref_train_inputs(1, 4096, 768, dev, N)
+        leaves = [x[0].requires_grad_(True), torch.ones(1, 4096, 768, device=dev, requires_grad=True) * 0.01] + \
+                 [t.requires_grad_(True) for t in x[2:]]  # delta as the reference builds it (not a leaf)
+        out, h = k.forward_with_state(*leaves)
+        fwd_mb = torch.cuda.max_memory_allocated() / 2**20
+        (out.sum() + h.sum()).backward()
+        res["memory_fp32_B1_L4096_D768"].append({"name": name, "forward_mb": fwd_mb,
+                                                  "total_mb": torch.cuda.max_memory_allocated() / 2**20,
+                                                  "reference_rtx5070_forward_total_mb": REF_MEM_MB[name]})
+        del x, leaves, out, h
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -673,6 +773,8 @@ def main():
                     help="storage dtype of the fwd+bwd step (default: the config's)")
     ap.add_argument("--profile-recipe", metavar="DIR", default=None,
                     help="print the rocprofv3 commands whose output --summarize turns into profiles/*.txt")
+    ap.add_argument("--reference-suite", action="store_true",
+                    help="run the reference's benchmark.py procedures (forward fp16, fwd+bwd fp32, memory)")
     ap.add_argument("--summarize", metavar="DIR", default=None,
                     help="write profiles/*.txt from the rocprofv3 CSV output in DIR (no GPU needed)")
     args = ap.parse_args()
@@ -693,6 +795,9 @@ def main():
         sys.exit(1)
     if args.kernels_only:
         print(json.dumps(kernels_only(args.config if args.config in ("cfg2", "cfg3") else "cfg2")))
+        return
+    if args.reference_suite:
+        print(json.dumps(reference_suite()))
         return
     if args.decode is not None:
         res = bench_decode(args.config if args.config in ("cfg2", "cfg3") else "cfg2", args.steps, args.warmup,
