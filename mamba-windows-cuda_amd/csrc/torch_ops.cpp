@@ -65,12 +65,15 @@ std::string shape_str(at::IntArrayRef s) {  // as Python prints a shape tuple: (
 bool last_dim_contiguous(const Tensor& t) { return t.dim() == 0 || t.stride(-1) == 1 || t.size(-1) == 1; }
 
 // The reference's input contract (mamba_cuda.py:281-326; N widened to 8, 16, 32, 64, bf16 storage
-// accepted), checked in the same order and with the same messages as ops.check_ssm_inputs.
+// accepted), with the same messages.
+// require_device = false skips the device-type checks (the contract can then be exercised with host
+// tensors).
 void check_ssm_inputs(const Tensor& u, const Tensor& delta, const Tensor& A, const Tensor& B, const Tensor& C,
-                      const Tensor& D, const OptT& h_prev) {
+                      const Tensor& D, const OptT& h_prev, bool require_device = true) {
     const std::pair<const char*, const Tensor*> named[] = {{"u", &u}, {"delta", &delta}, {"A", &A},
                                                            {"B_ssm", &B}, {"C_ssm", &C}, {"D_ssm", &D}};
-    for (const auto& [name, t] : named) TORCH_CHECK(t->is_cuda(), name, " must be a CUDA tensor");
+    if (require_device)
+        for (const auto& [name, t] : named) TORCH_CHECK(t->is_cuda(), name, " must be a CUDA tensor");
     const auto dt = u.scalar_type();
     TORCH_CHECK(dt == at::kFloat || dt == at::kHalf || dt == at::kBFloat16, "u must be float32/float16 (or bfloat16)");
     for (size_t i = 1; i < 6; ++i)
@@ -94,7 +97,7 @@ void check_ssm_inputs(const Tensor& u, const Tensor& delta, const Tensor& A, con
         TORCH_CHECK(named[i].second->device() == u.device(), "all inputs must be on the same device");
     if (h_prev.has_value()) {
         const Tensor& h = *h_prev;
-        TORCH_CHECK(h.is_cuda(), "h_prev must be a CUDA tensor");
+        TORCH_CHECK(!require_device || h.is_cuda(), "h_prev must be a CUDA tensor");
         TORCH_CHECK(h.scalar_type() == dt, "h_prev dtype must match u dtype");
         TORCH_CHECK(last_dim_contiguous(h), "h_prev must be contiguous in the last dimension");
         TORCH_CHECK(h.dim() == 3, "h_prev must be 3D (batch, dim, state)");
@@ -103,7 +106,7 @@ void check_ssm_inputs(const Tensor& u, const Tensor& delta, const Tensor& A, con
     }
 }
 
-// delta_bias (D,) and z (B, L, D), as ops.check_transforms.
+// delta_bias (D,) and z (B, L, D).
 void check_transforms(const Tensor& u, const OptT& delta_bias, const OptT& z) {
     const std::tuple<const char*, const OptT*, std::vector<int64_t>> items[] = {
         {"delta_bias", &delta_bias, {u.size(2)}}, {"z", &z, {u.size(0), u.size(1), u.size(2)}}};
@@ -122,7 +125,7 @@ struct FwdOut {
     Tensor out, out_ungated, h_last, ckpt;
 };
 
-// mwc_ssm_fwd_ex on contiguous copies of the inputs (as ops.ssm_forward_xf). `out` is the gated
+// mwc_ssm_fwd_ex on contiguous copies of the inputs. `out` is the gated
 // output when z is given, out_ungated the scan's own output (with z and want_ungated).
 FwdOut fwd_raw(const Tensor& u_, const Tensor& delta_, const Tensor& A_, const Tensor& B_, const Tensor& C_,
                const Tensor& D_, const OptT& h_prev_, const OptT& delta_bias_, bool softplus, const OptT& z_,
@@ -155,11 +158,12 @@ struct BwdOut {
     Tensor du, ddelta, dA, dB, dC, dD, dh_prev, dbias, dz;
 };
 
-// mwc_ssm_bwd_ex (as ops.ssm_backward_xf): dout and dh_last in u's dtype, the checkpoints of the
+// mwc_ssm_bwd_ex: dout and dh_last in u's dtype, the checkpoints of the
 // same inputs, the ungated forward output when z is given.
 BwdOut bwd_raw(const Tensor& u_, const Tensor& delta_, const Tensor& A_, const Tensor& B_, const Tensor& C_,
                const Tensor& D_, const Tensor& dout_, const Tensor& ckpt, const Tensor& dh_last_, bool want_dh_prev,
                const OptT& delta_bias_, bool softplus, const OptT& z_, const Tensor& out_ungated_) {
+    check_ssm_inputs(u_, delta_, A_, B_, C_, D_, std::nullopt);
     const Tensor u = u_.contiguous(), delta = delta_.contiguous(), A = A_.contiguous(), B = B_.contiguous(),
                  C = C_.contiguous(), D = D_.contiguous();
     const int64_t bsz = u.size(0), L = u.size(1), dm = u.size(2), n = A.size(1);
@@ -269,7 +273,39 @@ std::tuple<Tensor, Tensor> scan_autograd(const Tensor& u, const Tensor& delta, c
     return {r[0], r[1]};
 }
 
-// One decode step (as ops.ssm_step): u, delta, z (B, D); A (D, N); B_ssm, C_ssm (B, N); D_ssm (D,);
+// The raw operators behind ops.py (the Python host path of the reference-named autograd Functions):
+// no autograd of their own, outputs that a call does not ask for come back as None.
+void check_inputs_op(const Tensor& u, const Tensor& delta, const Tensor& A, const Tensor& B, const Tensor& C,
+                     const Tensor& D, const OptT& h_prev, bool require_device) {
+    check_ssm_inputs(u, delta, A, B, C, D, h_prev, require_device);
+}
+
+void check_transforms_op(const Tensor& u, const OptT& delta_bias, const OptT& z) {
+    TORCH_CHECK(u.dim() == 3, "u must be 3D (batch, seqlen, dim)");
+    check_transforms(u, delta_bias, z);
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor> fwd_op(const Tensor& u, const Tensor& delta, const Tensor& A,
+                                                  const Tensor& B, const Tensor& C, const Tensor& D,
+                                                  const OptT& h_prev, const OptT& delta_bias, bool softplus,
+                                                  const OptT& z, bool want_out, bool want_ungated, bool want_h_last,
+                                                  bool want_ckpt) {
+    FwdOut r = fwd_raw(u, delta, A, B, C, D, h_prev, delta_bias, softplus, z, want_out, want_ungated, want_h_last,
+                       want_ckpt);
+    return {r.out, r.out_ungated, r.h_last, r.ckpt};
+}
+
+using Grads9 = std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor>;
+
+Grads9 bwd_op(const Tensor& u, const Tensor& delta, const Tensor& A, const Tensor& B, const Tensor& C, const Tensor& D,
+              const Tensor& dout, const OptT& ckpt, const OptT& dh_last, bool want_dh_prev, const OptT& delta_bias,
+              bool softplus, const OptT& z, const OptT& out_ungated) {
+    BwdOut g = bwd_raw(u, delta, A, B, C, D, dout, ckpt.value_or(Tensor()), dh_last.value_or(Tensor()), want_dh_prev,
+                       delta_bias, softplus, z, out_ungated.value_or(Tensor()));
+    return {g.du, g.ddelta, g.dA, g.dB, g.dC, g.dD, g.dh_prev, g.dbias, g.dz};
+}
+
+// One decode step: u, delta, z (B, D); A (D, N); B_ssm, C_ssm (B, N); D_ssm (D,);
 // h (B, D, N). Returns (out (B, D), gated by silu(z) when z is given, h_new); out_state, when given,
 // receives h_new and may be h itself (an in-place update). Inference only.
 std::tuple<Tensor, Tensor> step_impl(const Tensor& u_, const Tensor& delta_, const Tensor& A_, const Tensor& B_,
@@ -337,9 +373,26 @@ std::tuple<Tensor, Tensor> step_autograd(const Tensor& u, const Tensor& delta, c
 TORCH_LIBRARY(mwc, m) {
     m.def("ssm_scan(Tensor u, Tensor delta, Tensor A, Tensor B_ssm, Tensor C_ssm, Tensor D_ssm, Tensor? h_prev=None, "
           "int checkpoint_lvl=0, Tensor? z=None, Tensor? delta_bias=None, bool delta_softplus=False) -> (Tensor, Tensor)");
+    m.def("check_ssm_inputs(Tensor u, Tensor delta, Tensor A, Tensor B_ssm, Tensor C_ssm, Tensor D_ssm, "
+          "Tensor? h_prev=None, bool require_device=True) -> ()");
+    m.def("check_transforms(Tensor u, Tensor? delta_bias=None, Tensor? z=None) -> ()");
+    m.def("ssm_fwd(Tensor u, Tensor delta, Tensor A, Tensor B_ssm, Tensor C_ssm, Tensor D_ssm, Tensor? h_prev, "
+          "Tensor? delta_bias, bool delta_softplus, Tensor? z, bool want_out, bool want_ungated, bool want_h_last, "
+          "bool want_ckpt) -> (Tensor, Tensor, Tensor, Tensor)");
+    m.def("ssm_bwd(Tensor u, Tensor delta, Tensor A, Tensor B_ssm, Tensor C_ssm, Tensor D_ssm, Tensor dout, "
+          "Tensor? ckpt, Tensor? dh_last, bool want_dh_prev, Tensor? delta_bias, bool delta_softplus, Tensor? z, "
+          "Tensor? out_ungated) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)");
     m.def("ssm_step(Tensor u, Tensor delta, Tensor A, Tensor B_ssm, Tensor C_ssm, Tensor D_ssm, Tensor h, "
           "Tensor? z=None, Tensor? delta_bias=None, bool delta_softplus=False, Tensor(a!)? out_state=None) "
           "-> (Tensor, Tensor)");
+}
+
+// the raw operators run below autograd on every backend (host tensors reach the checks and are refused)
+TORCH_LIBRARY_IMPL(mwc, CompositeImplicitAutograd, m) {
+    m.impl("check_ssm_inputs", &check_inputs_op);
+    m.impl("check_transforms", &check_transforms_op);
+    m.impl("ssm_fwd", &fwd_op);
+    m.impl("ssm_bwd", &bwd_op);
 }
 
 TORCH_LIBRARY_IMPL(mwc, Autograd, m) {

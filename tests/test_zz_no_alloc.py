@@ -10,6 +10,10 @@ import torch
 from mamba_windows_cuda import _lib, ops, workloads
 
 
+def _p(t):
+    return None if t is None else t.data_ptr()
+
+
 def _fwd_both(dev, B, L, D, dtype, *, xf, seed):
     x = {k: v.to(dev) for k, v in workloads.ssm_inputs(B, L, D, dtype=dtype, h_prev=True, dout=False,
                                                        seed=seed).items()}
@@ -27,7 +31,7 @@ def _fwd_both(dev, B, L, D, dtype, *, xf, seed):
         ckpt = torch.full((B, nck, D, 16), float("nan"), dtype=torch.float32, device=dev)
         args = (ops._dtype_code(x["u"]), x["u"].data_ptr(), x["delta"].data_ptr(), x["A"].data_ptr(),
                 x["B"].data_ptr(), x["C"].data_ptr(), x["D"].data_ptr(), x["h_prev"].data_ptr(),
-                ops._ptr(bias), int(xf), ops._ptr(z), out.data_ptr(), ops._ptr(out_z), h_last.data_ptr(),
+                _p(bias), int(xf), _p(z), out.data_ptr(), _p(out_z), h_last.data_ptr(),
                 ckpt.data_ptr(), B, L, D, 16)
         if which == "ex":
             ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
