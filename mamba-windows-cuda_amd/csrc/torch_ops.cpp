@@ -167,6 +167,10 @@ BwdOut bwd_raw(const Tensor& u_, const Tensor& delta_, const Tensor& A_, const T
     const Tensor u = u_.contiguous(), delta = delta_.contiguous(), A = A_.contiguous(), B = B_.contiguous(),
                  C = C_.contiguous(), D = D_.contiguous();
     const int64_t bsz = u.size(0), L = u.size(1), dm = u.size(2), n = A.size(1);
+    // every operand the kernels read must live on u's device
+    for (const auto& [name, t] : {std::pair<const char*, const Tensor*>{"dout", &dout_}, {"dh_last", &dh_last_},
+                                  {"ckpt", &ckpt}, {"out_ungated", &out_ungated_}})
+        TORCH_CHECK(!t->defined() || t->device() == u_.device(), name, " must be on the same device as u");
     const Tensor dout = dout_.to(u.scalar_type()).contiguous();
     TORCH_CHECK(dout.sizes() == u.sizes(), "dout shape mismatch");
     Tensor dh_last;
@@ -343,10 +347,10 @@ std::tuple<Tensor, Tensor> step_impl(const Tensor& u_, const Tensor& delta_, con
     const Tensor A = aligned(A_), B = aligned(B_), C = aligned(C_), h = aligned(h_);
     const Tensor delta_bias = contig(delta_bias_), z = contig(z_);
     Tensor h_new = out_state.has_value() ? *out_state : at::empty_like(h);
-    TORCH_CHECK(h_new.is_contiguous() && h_new.dim() == 3 && h_new.size(0) == bsz && h_new.size(1) == dm &&
-                    h_new.size(2) == n && h_new.scalar_type() == dt &&
+    TORCH_CHECK(h_new.device() == u_.device() && h_new.is_contiguous() && h_new.dim() == 3 && h_new.size(0) == bsz &&
+                    h_new.size(1) == dm && h_new.size(2) == n && h_new.scalar_type() == dt &&
                     reinterpret_cast<uintptr_t>(h_new.data_ptr()) % 16 == 0,
-                "out_state must be a contiguous, 16-byte-aligned (B, D, N) tensor of u's dtype");
+                "out_state must be a contiguous, 16-byte-aligned (B, D, N) tensor of u's dtype and device");
     c10::hip::HIPGuardMasqueradingAsCUDA guard(u.device());
     const Tensor out = at::empty_like(u);
     check_status(mwc_ssm_step(dtype_code(u), ptr(u), ptr(delta), ptr(A), ptr(B), ptr(C), ptr(D), ptr(h),

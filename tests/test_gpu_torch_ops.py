@@ -156,3 +156,23 @@ def test_step_operator_equals_python_step(dev, dtype, xf):
     y4, h4 = m.step(args[0], args[1], A_mis, *args[3:], h_mis, **kw)
     torch.cuda.synchronize()
     assert torch.equal(y4, y1) and torch.equal(h4, h1)
+
+
+def test_operands_on_another_device_are_refused(dev):
+    """Every operand a kernel reads must be on u's device: a host dout, dh_last, checkpoint or
+    out_state raises RuntimeError before anything is enqueued."""
+    from mamba_windows_cuda import ops
+
+    x = {k: v.to(dev) for k, v in workloads.ssm_inputs(1, 40, 32, h_prev=True, seed=4).items()}
+    _, _, h_last, ckpt = ops.ssm_forward_xf(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], want_ckpt=True)
+    args = (x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"])
+    with pytest.raises(RuntimeError, match="dout must be on the same device"):
+        ops.ssm_backward(*args, x["dout"].cpu(), ckpt)
+    with pytest.raises(RuntimeError, match="dh_last must be on the same device"):
+        ops.ssm_backward(*args, x["dout"], ckpt, h_last.cpu())
+    with pytest.raises(RuntimeError, match="ckpt must be on the same device"):
+        ops.ssm_backward(*args, x["dout"], ckpt.cpu())
+    step_args = (x["u"][:, 0], x["delta"][:, 0], x["A"], x["B"][:, 0], x["C"][:, 0], x["D"], x["h_prev"])
+    with pytest.raises(RuntimeError, match="out_state must be"):
+        SelectiveScanCuda().step(*step_args, out_state=torch.zeros(1, 32, 16))
+    torch.cuda.synchronize()
