@@ -183,3 +183,39 @@ def test_long_fp16_single_pass(dev, shape):
     ro, _ = orc.ssm_fwd(u[:, :, :k].cpu(), delta[:, :, :k].cpu(), A[:k].cpu(), Bs.cpu(), Cs.cpu(), Dv[:k].cpu(),
                         None, clamp=True)
     np.testing.assert_allclose(_np(out[:, :, :k]), ro, **TOL[torch.float16])
+
+
+def test_beyond_2_31_elements(dev):
+    """B*L*D = 2^32 fp16 elements (B=2, L=2^20, D=2048; batch row 1 starts 2^31 elements in): the fused
+    forward and backward address every tensor with 64-bit offsets. Checked by a property of the scan:
+    the last 4096 steps of row 1 equal a separate fp32 call on those steps started from the forward's
+    checkpoint state, and so do their du, ddelta, dB and dC (the adjoint at a step depends only on later
+    steps). The inputs take ~26 GB, the whole step ~90 GB of the 288 GB HBM."""
+    from mamba_windows_cuda import ops
+
+    Bsz, L, D, N, T = 2, 1 << 20, 2048, 16, 4096
+    print(f"case beyond 2^31 elements B={Bsz} L={L} D={D}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(31)
+    u = torch.randn(Bsz, L, D, generator=g, device=dev, dtype=torch.float16)
+    delta = torch.rand(Bsz, L, D, generator=g, device=dev, dtype=torch.float16).mul_(0.099).add_(0.001)
+    A = -(0.01 + 0.99 * torch.rand(D, N, generator=g, device=dev)).half()
+    Bs = torch.randn(Bsz, L, N, generator=g, device=dev, dtype=torch.float16)
+    Cs = torch.randn(Bsz, L, N, generator=g, device=dev, dtype=torch.float16)
+    Dv = (1.0 + 0.1 * torch.randn(D, generator=g, device=dev)).half()
+    out, _, ckpt = ops.ssm_forward(u, delta, A, Bs, Cs, Dv, want_h_last=False, want_ckpt=True)
+    t0 = L - T
+    h0 = ckpt[1:2, t0 // 16].clone()  # fp32 state before step t0 of row 1
+    tail = [t[1:2, t0:].float() for t in (u, delta)] + [A.float()] + [t[1:2, t0:].float() for t in (Bs, Cs)] + \
+        [Dv.float()]
+    ref_out, _, ref_ckpt = ops.ssm_forward(*tail, h0, want_h_last=False, want_ckpt=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out[1, t0:]).all()
+    torch.testing.assert_close(out[1:2, t0:].float(), ref_out, **TOL[torch.float16])
+    dout = torch.randn(Bsz, L, D, generator=g, device=dev, dtype=torch.float16)
+    du, ddelta, _, dB, dC, _, _ = ops.ssm_backward(u, delta, A, Bs, Cs, Dv, dout, ckpt)
+    del ckpt
+    rdu, rdd, _, rdB, rdC, _, _ = ops.ssm_backward(*tail, dout[1:2, t0:].float(), ref_ckpt, None, False)
+    torch.cuda.synchronize()
+    for name, got, ref in (("du", du, rdu), ("ddelta", ddelta, rdd), ("dB", dB, rdB), ("dC", dC, rdC)):
+        assert torch.isfinite(got[1, t0:]).all(), name
+        torch.testing.assert_close(got[1:2, t0:].float(), ref, msg=name, **TOL[torch.float16])
