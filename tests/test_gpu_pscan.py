@@ -57,3 +57,36 @@ def test_pscan_config4b(dev):
     torch.cuda.synchronize()
     ref = orc.pscan_fwd(a, b)
     np.testing.assert_allclose(_np(H), ref, rtol=1e-3, atol=1e-4)
+
+
+def test_scan_beyond_2_31_elements(dev):
+    """(4, 2^20, 1024) fp32, 2^32 elements per tensor (the last sequence starts 3*2^30 elements in, its
+    look-back chains are 8192 tiles long): the forward and the adjoint address with 64-bit offsets.
+    Checked by restarting the scan: the last 4096 steps of the last sequence equal a scan of those
+    steps whose first input folds in the state before them, and the adjoint's last steps equal the
+    adjoint of that shorter scan (it depends only on later steps)."""
+    from mamba_windows_cuda.pscan import pscan_check
+
+    S, L, C, T = 4, 1 << 20, 1024, 4096
+    print(f"case scan beyond 2^31 elements ({S}, {L}, {C})", flush=True)
+    g = torch.Generator(device=dev).manual_seed(5)
+    A = torch.rand(S, L, C, generator=g, device=dev).mul_(0.1).add_(0.9).requires_grad_(True)
+    X = torch.randn(S, L, C, generator=g, device=dev).requires_grad_(True)
+    H = parallel_scan_fn(A, X)
+    dH = torch.randn(S, L, C, generator=g, device=dev)
+    H.backward(dH)
+    t0 = L - T
+    with torch.no_grad():
+        At = A[S - 1:, t0:].clone()
+        Xt = X[S - 1:, t0:].clone()
+        Xt[:, 0] += At[:, 0] * H[S - 1:, t0 - 1]
+    At.requires_grad_(True)
+    Xt.requires_grad_(True)
+    Ht = parallel_scan_fn(At, Xt)
+    Ht.backward(dH[S - 1:, t0:])
+    pscan_check()
+    torch.cuda.synchronize()
+    torch.testing.assert_close(H[S - 1:, t0:], Ht, rtol=1e-4, atol=1e-4)
+    torch.testing.assert_close(X.grad[S - 1:, t0:], Xt.grad, rtol=1e-4, atol=1e-4)
+    # dA_t = g_t * H_{t-1}: the restarted scan's first step has no H_{t-1} of its own
+    torch.testing.assert_close(A.grad[S - 1:, t0 + 1:], At.grad[:, 1:], rtol=1e-4, atol=1e-4)
