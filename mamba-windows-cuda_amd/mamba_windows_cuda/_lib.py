@@ -1,10 +1,11 @@
-"""ctypes binding of libmwc_ssm.so, the gfx950 C-ABI library (include/mwc_ssm.h).
+"""Loading of the native libraries: the ctypes binding of libmwc_ssm.so, the gfx950 C-ABI library
+(include/mwc_ssm.h), and libmwc_torch.so, its PyTorch operators (torch.ops.mwc.*).
 
 This replaces the reference's JIT bootstrap (``_get_selective_scan_cuda_module``,
 mamba_windows_cuda/mamba_cuda.py:832-872; ``_get_fused_module``,
-selective_scan_cuda_ext.py:530-559): the library is built ahead of time with
-hipcc for gfx950 and only loaded here. If it is missing the import of the
-operators fails loudly -- there is no CPU or PyTorch fallback.
+selective_scan_cuda_ext.py:530-559): the libraries are built ahead of time with
+hipcc and only loaded here. If one is missing its first use fails loudly -- there is
+no CPU or PyTorch fallback.
 """
 from __future__ import annotations
 

@@ -3,7 +3,8 @@
 
 Same public names, signatures, shapes and dtype rules as the reference
 (mamba_windows_cuda/mamba_cuda.py:1044-1219); the work runs in the gfx950
-kernels of libmwc_ssm.so through the C ABI (see ops.py). Differences from the
+kernels of libmwc_ssm.so, called through the PyTorch operators of libmwc_torch.so
+(csrc/torch_ops.cpp). Differences from the
 reference, all in the direction of correctness:
 
 * one fused forward and one fused backward serve every mode. The stateful
@@ -27,7 +28,7 @@ import torch
 from . import _lib, ops
 
 _scan_op = None
-_step_op = None  # torch.ops.mwc.ssm_step: the decode step's checks and launch in C++ (as ops.ssm_step)
+_step_op = None  # torch.ops.mwc.ssm_step: the decode step's checks and launch in C++
 
 
 def _ssm_scan(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, checkpoint_lvl, z, delta_bias, delta_softplus):
@@ -79,9 +80,9 @@ class SelectiveScanCudaFunction(torch.autograd.Function):
     delta_softplus=False) -> (out, h_last); backward returns dh_prev when h_prev is given
     (mamba_cuda.py:1044-1096). The last three arguments are the fused transforms (delta' =
     softplus(delta + delta_bias), out = scan * silu(z)); the reference has no counterpart.
-    This is the Python host path (ops.py over ctypes); SelectiveScanCuda and FusedSelectiveScan
-    call the C++ operator ``torch.ops.mwc.ssm_scan``, which runs the same kernels with the same
-    checks and gives bitwise the same results with less host time per call."""
+    A Python autograd Function over the raw operators (ops.ssm_forward_xf / ssm_backward_xf);
+    SelectiveScanCuda and FusedSelectiveScan call ``torch.ops.mwc.ssm_scan``, whose autograd
+    Function is C++, with bitwise the same results and less host time per call."""
 
     @staticmethod
     def forward(ctx, u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, checkpoint_lvl=0, z=None, delta_bias=None,
