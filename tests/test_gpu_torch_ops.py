@@ -176,3 +176,41 @@ def test_operands_on_another_device_are_refused(dev):
     with pytest.raises(RuntimeError, match="out_state must be"):
         SelectiveScanCuda().step(*step_args, out_state=torch.zeros(1, 32, 16))
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("lvl", [0, 1])
+def test_strided_views_equal_contiguous_copies(dev, lvl):
+    """Inputs that are views with a contiguous last dimension but other strides (an L-slice with B > 1,
+    a D-slice of a wider tensor, A as the first 16 columns of a (D, 32) tensor, a B-slice of h_prev):
+    the operator copies them to contiguous tensors first, as the reference does
+    (mamba_cuda.py:1197-1199), so outputs and the gradients reaching the base tensors equal those of
+    contiguous copies, bitwise."""
+    print(f"case strided views lvl={lvl}", flush=True)
+    g = torch.Generator().manual_seed(12)
+    Bsz, L, D, N = 3, 200, 96, 16
+    base = {"u": torch.randn(Bsz, L + 50, D + 8, generator=g),
+            "delta": 0.01 + 0.09 * torch.rand(Bsz, L + 50, D + 8, generator=g),
+            "A": -torch.rand(D, 2 * N, generator=g), "B": torch.randn(Bsz, L + 50, N, generator=g),
+            "C": torch.randn(Bsz, L + 50, N, generator=g), "D": torch.randn(D, generator=g),
+            "h_prev": torch.randn(Bsz + 1, D, N, generator=g)}
+    dout = torch.randn(Bsz, L, D, generator=g).to(dev)
+
+    def views(t):
+        return (t["u"][:, 20:20 + L, 4:4 + D], t["delta"][:, 20:20 + L, 4:4 + D], t["A"][:, :N],
+                t["B"][:, 20:20 + L], t["C"][:, 20:20 + L], t["D"], t["h_prev"][1:])
+
+    res = []
+    for contiguous in (False, True):
+        leaves = {k: v.to(dev).requires_grad_(True) for k, v in base.items()}
+        args = views(leaves)
+        assert contiguous or not all(a.is_contiguous() for a in args)
+        if contiguous:
+            args = tuple(a.contiguous() for a in args)
+        out, h_last = SelectiveScanCuda(checkpoint_lvl=lvl).forward_with_state(*args)
+        ((out * dout).sum() + h_last.sum()).backward()
+        torch.cuda.synchronize()
+        res.append((out.detach(), h_last.detach(), {k: t.grad for k, t in leaves.items()}))
+    (o1, h1, g1), (o2, h2, g2) = res
+    assert torch.equal(o1, o2) and torch.equal(h1, h2)
+    for k in g1:
+        assert torch.equal(g1[k], g2[k]), k
