@@ -185,8 +185,9 @@ def bench_ssm(cfg, steps, warmup, level, shard=1, nstate=16, dtype_name=None, gr
     # HBM bytes the counters measured for one backward call (committed rocprofv3 --pmc summary), and the
     # VALU instructions its main kernel issued per state and step (SQ_INSTS_VALU x 64 lanes / states)
     traffic = _traffic_from_profiles(f"ssm_bwd_{cfg}") if default_case else None
-    valu_instr = _pmc_field(f"ssm_bwd_{cfg}", "main_kernel_valu_instructions_per_state_step") if default_case else None
-    valu_instr_fwd = _pmc_field(f"ssm_fwd_{cfg}", "main_kernel_valu_instructions_per_state_step") if default_case else None
+    key = "main_kernel_valu_instructions_per_state_step"
+    valu_instr = _pmc_field(f"ssm_bwd_{cfg}", key) if default_case else None
+    valu_instr_fwd = _pmc_field(f"ssm_fwd_{cfg}", key) if default_case else None
     sdt = {torch.float16: "f16", torch.bfloat16: "bf16"}.get(dtype, "f32")
     res = {
         "metric": METRIC,
@@ -312,7 +313,8 @@ def bench_decode(cfg, steps, warmup, batch=None):
     nbytes = s * (2 * B * D * 16 + 3 * B * D + 2 * B * 16 + D * 16 + D)
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"metric": "decode steps/s (L=1, state in place, HIP-graph replay)", "value": 1e3 / ms,
-            "unit": "steps/s", "us_per_step": ms * 1e3, "us_per_step_eager": ms_eager * 1e3, "dtype": "f32", "storage_dtype": "f16" if s == 2 else "f32",
+            "unit": "steps/s", "us_per_step": ms * 1e3, "us_per_step_eager": ms_eager * 1e3, "dtype": "f32",
+            "storage_dtype": "f16" if s == 2 else "f32",
             "config": {"workload": f"{cfg} decode step, B={B} D={D} N=16", "B": B, "D": D, "N": 16},
             "roofline": {"bound": "hbm", "kernel": "ssm_step_kernel", "achieved": gbs, "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "algorithmic_bytes_per_launch": nbytes}}
