@@ -489,6 +489,7 @@ TRACE_RUNS = {
     "cfg4a_stream": ["--config", "cfg4a", "--steps", "10"],
     "cfg4b_pscan": ["--config", "cfg4b", "--steps", "50", "--skip-cpu"],
     "decode_b1024": ["--decode", "1024", "--steps", "320"],
+    "shard8_eager": ["--shard", "8", "--steps", "400"],
 }
 PMC_PASSES = {
     "fetch": "FETCH_SIZE",
