@@ -357,6 +357,10 @@ std::tuple<Tensor, Tensor> step_impl(const Tensor& u_, const Tensor& delta_, con
                               ptr(delta_bias), softplus ? 1 : 0, ptr(z), z.defined() ? nullptr : ptr(out),
                               z.defined() ? ptr(out) : nullptr, ptr(h_new), bsz, dm, n, stream_of(u)),
                  "mwc_ssm_step");
+    // the kernel wrote out_state through a raw pointer: bump its version counter as an in-place op
+    // would, so autograd sees the overwrite of a state some other op saved (the op is eager-only: no
+    // Meta kernel or aliasing information for functionalization / torch.compile)
+    if (out_state.has_value()) torch::autograd::impl::bump_version(*out_state);
     return {out, h_new};
 }
 

@@ -14,6 +14,8 @@ import os
 import threading
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
+# MWC_SSM_LIB: another build of libmwc_ssm.so, used by the ctypes binding and (through its SONAME) by
+# the PyTorch operators alike
 LIB_PATH = os.environ.get("MWC_SSM_LIB", os.path.join(_HERE, "libmwc_ssm.so"))
 
 MWC_DTYPE_F32 = 0
@@ -23,7 +25,7 @@ MWC_OK = 0
 CKPT_STEPS = 16  # MWC_CKPT_STEPS
 NOALLOC_SCRATCH_BYTES = 32 << 20  # MWC_NOALLOC_SCRATCH_BYTES
 
-_lock = threading.Lock()
+_lock = threading.RLock()  # torch_ops() loads the C-ABI library under it
 _lib = None
 
 P = ctypes.c_void_p
@@ -106,6 +108,10 @@ def torch_ops():
                     "or `make -C mamba-windows-cuda_amd/csrc`")
             import torch
 
+            # load the C-ABI library first (from LIB_PATH, which MWC_SSM_LIB may point elsewhere): its
+            # SONAME then satisfies libmwc_torch.so's dependency, so the operators and the ctypes
+            # binding share one copy instead of the RUNPATH one being mapped as well
+            lib()
             torch.ops.load_library(TORCH_OPS_PATH)
             _torch_ops = torch.ops.mwc
     return _torch_ops

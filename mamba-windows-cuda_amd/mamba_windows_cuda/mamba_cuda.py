@@ -199,7 +199,27 @@ def selective_scan_ref(u, delta, A, B_ssm, C_ssm, D_ssm, h_prev=None, return_int
     return out, h
 
 
-def selective_scan_backward(dout, dh_last, intermediates, D_ssm):
+def recover_A(dA, delta_t):
+    """A (D, N) from the reference intermediates' decay factors dA = exp(delta*A) (B, D, N, L) and
+    delta_t (B, D, L): A = log(dA) / delta at, for each (d, n), the (b, t) with the largest delta
+    whose factor is a normal number (log(dA) then carries an absolute error of about one ulp of 1,
+    so A's absolute error is about eps / delta: 7e-7 at delta = 0.09 in fp32). Raises
+    RuntimeError for a (d, n) with no usable step (delta = 0 everywhere, where the decay factors do
+    not depend on A, or every factor underflowed); pass A explicitly then."""
+    bsz, dm, n, L = dA.shape
+    dl = delta_t.unsqueeze(2).expand(bsz, dm, n, L)
+    usable = (dl > 0) & (dA >= torch.finfo(dA.dtype).tiny) & torch.isfinite(dA)
+    score = torch.where(usable, dl, torch.full_like(dl, -1.0))
+    score = score.permute(1, 2, 0, 3).reshape(dm, n, bsz * L)
+    best = score.argmax(-1, keepdim=True)
+    if not bool((score.gather(-1, best) > 0).all()):
+        raise RuntimeError("selective_scan_backward: A cannot be recovered from intermediates['dA'] for every "
+                           "(d, n) (delta is 0 or the decay factors underflow); pass A=")
+    pick = lambda x: x.permute(1, 2, 0, 3).reshape(dm, n, bsz * L).gather(-1, best).squeeze(-1)
+    return torch.log(pick(dA)) / pick(dl)
+
+
+def selective_scan_backward(dout, dh_last, intermediates, D_ssm, A=None):
     """Gradients of the selective scan from ``selective_scan_ref``'s intermediates: the reference
     API (mamba_cuda.py:949-1041), same arguments and return order
     ``(du, ddelta, dA, dB_ssm, dC_ssm, dD_ssm, dh_prev)``; plain PyTorch on the intermediates'
@@ -214,13 +234,14 @@ def selective_scan_backward(dout, dh_last, intermediates, D_ssm):
       du = D*dout + delta*sum_n g*B          ddelta = sum_n g*(A*dA_t*h_{t-1} + u*B)
       dA = sum_{b,t} delta*g*dA_t*h_{t-1}    dB = sum_d g*delta*u    dC = sum_d dout*h_t
       dD = sum_{b,t} dout*u                  dh_prev = dA_0*g_0
-    ``intermediates`` must also hold 'A' (D, N), which ``selective_scan_ref`` adds; ``dh_last``
-    may be None (zeros)."""
+    The ddelta term needs A itself: it is taken from the ``A`` keyword, else from
+    intermediates['A'] (which ``selective_scan_ref`` here adds), else recovered from the reference's
+    8-key dict (mamba_cuda.py:934-944) by ``recover_A``. ``dh_last`` may be None (zeros)."""
     h_states, dA_t, u_t, d_t = (intermediates[k] for k in ("h_states", "dA", "u_t", "delta_t"))
     B_t, C_t, h_prev = intermediates["B_t"], intermediates["C_t"], intermediates["h_prev"]
-    if "A" not in intermediates:
-        raise RuntimeError("selective_scan_backward needs intermediates['A'] (selective_scan_ref adds it)")
-    A = intermediates["A"]
+    if A is None:
+        A = intermediates["A"] if "A" in intermediates else recover_A(dA_t, d_t)
+    A = A.to(h_states.dtype)
     bsz, dm, n, L = h_states.shape
     dout_t = dout.transpose(1, 2).to(h_states.dtype)      # (B, D, L)
     g = (torch.zeros_like(h_prev) if dh_last is None else dh_last.to(h_states.dtype)).clone()

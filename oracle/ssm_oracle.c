@@ -21,6 +21,10 @@
  *                         ddelta= sum_n g*(A*dA_t*h_{t-1} + u*B)
  *                         dA    = sum_{b,t} g*delta*dA_t*h_{t-1}
  *                         dD    = sum_{b,t} dout*u        dh_prev = dA_0*g_0
+ *                       plus, when dA_abs is not NULL, sum_{b,t} |g*delta*dA_t*h_{t-1}|:
+ *                       the sum of dA's terms' magnitudes, the scale of the rounding
+ *                       error that any fp32 evaluation of the sum carries (a
+ *                       conditioning measure for tests, not a gradient).
  *   oracle_pscan_fwd <- parallel_scan_ref, mamba_windows_cuda/pscan.py:153-171
  *                       (H_0 = X_0, A_0 ignored; H_t = A_t*H_{t-1} + X_t)
  *   oracle_pscan_bwd <- its adjoint: G~_t = dH_t + A_{t+1}*G~_{t+1};
@@ -92,12 +96,13 @@ void oracle_ssm_bwd(i64 Bsz, i64 L, i64 Dm, i64 N, const double* u, const double
                     const double* A, const double* Bm, const double* Cm, const double* Dv,
                     const double* h_prev, const double* dout, const double* dh_last, int clamp,
                     double* du, double* ddelta, double* dA, double* dB, double* dC, double* dD,
-                    double* dh_prev) {
+                    double* dh_prev, double* dA_abs) {
     const i64 nblk = (Dm + OR_BBLK - 1) / OR_BBLK;
     const i64 nitems = Bsz * nblk;
     /* per-item partials, summed afterwards in item order (deterministic) */
     double* pBC = (double*)calloc((size_t)nitems * L * N * 2, sizeof(double));
     double* pA = (double*)calloc((size_t)nitems * OR_BBLK * N, sizeof(double));
+    double* pAa = (double*)calloc((size_t)nitems * OR_BBLK * N, sizeof(double));
     double* pD = (double*)calloc((size_t)nitems * OR_BBLK, sizeof(double));
 #pragma omp parallel for schedule(dynamic, 1)
     for (i64 item = 0; item < nitems; ++item) {
@@ -131,6 +136,7 @@ void oracle_ssm_bwd(i64 Bsz, i64 L, i64 Dm, i64 N, const double* u, const double
         }
         double* myBC = pBC + (size_t)item * L * N * 2;
         double* myA = pA + (size_t)item * OR_BBLK * N;
+        double* myAa = pAa + (size_t)item * OR_BBLK * N;
         double* myD = pD + (size_t)item * OR_BBLK;
         for (i64 t = L - 1; t >= 0; --t) {
             const i64 row = (b * L + t) * Dm;
@@ -151,6 +157,7 @@ void oracle_ssm_bwd(i64 Bsz, i64 L, i64 Dm, i64 N, const double* u, const double
                     const double s = gt * e * prev;
                     r2 += A[d * N + n] * s;
                     myA[(d - d0) * N + n] += dt * s;
+                    myAa[(d - d0) * N + n] += fabs(dt * s);
                     g[k] = e * gt;
                 }
                 du[row + d] = Dv[d] * yo + dt * r1;
@@ -184,15 +191,20 @@ void oracle_ssm_bwd(i64 Bsz, i64 L, i64 Dm, i64 N, const double* u, const double
         const i64 blk = d / OR_BBLK, off = d % OR_BBLK;
         double sd = 0.0;
         for (i64 n = 0; n < N; ++n) {
-            double sa = 0.0;
-            for (i64 b = 0; b < Bsz; ++b) sa += pA[(size_t)(b * nblk + blk) * OR_BBLK * N + off * N + n];
+            double sa = 0.0, saa = 0.0;
+            for (i64 b = 0; b < Bsz; ++b) {
+                sa += pA[(size_t)(b * nblk + blk) * OR_BBLK * N + off * N + n];
+                saa += pAa[(size_t)(b * nblk + blk) * OR_BBLK * N + off * N + n];
+            }
             dA[d * N + n] = sa;
+            if (dA_abs) dA_abs[d * N + n] = saa;
         }
         for (i64 b = 0; b < Bsz; ++b) sd += pD[(size_t)(b * nblk + blk) * OR_BBLK + off];
         dD[d] = sd;
     }
     free(pBC);
     free(pA);
+    free(pAa);
     free(pD);
 }
 

@@ -52,6 +52,30 @@ def test_torch_operator_library_registers_ssm_scan():
                      torch.zeros(2, 3, 16))
 
 
+def test_library_override_maps_one_copy(tmp_path):
+    """With MWC_SSM_LIB pointing at another copy of libmwc_ssm.so, the ctypes binding and the PyTorch
+    operators (whose dependency resolves through the library's SONAME) share that one copy: the
+    process maps a single libmwc_ssm.so, the override."""
+    import shutil
+    import subprocess
+    import sys
+
+    from mamba_windows_cuda import _lib
+
+    alt = tmp_path / "libmwc_ssm.so"
+    shutil.copy(_lib.LIB_PATH, alt)
+    code = (
+        "import sys; sys.path[:0] = %r\n"
+        "from mamba_windows_cuda import _lib\n"
+        "_lib.torch_ops(); _lib.lib()\n"
+        "maps = {l.split()[-1] for l in open('/proc/self/maps') if l.rstrip().endswith('libmwc_ssm.so')}\n"
+        "print(sorted(maps))\n" % (sys.path[:3],))
+    env = dict(os.environ, MWC_SSM_LIB=str(alt))
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr
+    assert r.stdout.strip() == str([str(alt)]), r.stdout
+
+
 def test_status_strings_and_ckpt_count():
     from mamba_windows_cuda import _lib
 
@@ -264,9 +288,43 @@ def test_selective_scan_backward_is_the_true_adjoint():
     got0 = selective_scan_backward(dout, None, inter, Dv)
     ref0 = orc.ssm_bwd(u, delta, A, Bs, Cs, Dv, dout, hp, None)
     np.testing.assert_allclose(got0[6].numpy(), ref0["dh_prev"], rtol=1e-10, atol=1e-12)
+    # the reference's own 8-key dict (mamba_cuda.py:934-944, no 'A'): A recovered from dA and delta_t,
+    # or passed as a keyword
     inter.pop("A")
-    with pytest.raises(RuntimeError, match="intermediates"):
+    assert sorted(inter) == sorted(["h_states", "dA", "dBu", "u_t", "delta_t", "B_t", "C_t", "h_prev"])
+    for got in (selective_scan_backward(dout, dhl, inter, Dv), selective_scan_backward(dout, dhl, inter, Dv, A=A)):
+        for name, t in zip(names, got):
+            np.testing.assert_allclose(t.numpy(), ref[name], rtol=1e-10, atol=1e-12, err_msg=name)
+    # a channel whose delta is 0 at every step: its decay factors are 1 whatever A is
+    inter["delta_t"] = inter["delta_t"].clone()
+    inter["delta_t"][:, 2] = 0.0
+    with pytest.raises(RuntimeError, match="pass A="):
         selective_scan_backward(dout, dhl, inter, Dv)
+
+
+def test_selective_scan_backward_reference_dict_fp32():
+    """The reference's fp32 intermediates (config-0 distributions, delta ~ U(1e-3, 1e-1)) without 'A':
+    the recovered A (absolute error ~eps/max delta) keeps every gradient within the fp32 bound of the
+    float64 oracle."""
+    import numpy as np
+
+    from mamba_windows_cuda import workloads
+    from mamba_windows_cuda.mamba_cuda import recover_A, selective_scan_backward, selective_scan_ref
+    from oracle import oracle as orc
+
+    x = workloads.ssm_inputs(2, 64, 24, dtype=torch.float32, a_lo=0.0, a_hi=0.1, d_mode="ones", h_prev=True,
+                             seed=5)
+    dhl = torch.randn(2, 24, 16, generator=torch.Generator().manual_seed(6))
+    _, _, inter = selective_scan_ref(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["h_prev"],
+                                     return_intermediates=True)
+    inter.pop("A")
+    Ar = recover_A(inter["dA"], inter["delta_t"])
+    # log(dA) carries about one ulp of 1: an absolute error in A of ~eps32/max(delta) = 7e-7
+    np.testing.assert_allclose(Ar.numpy(), x["A"].numpy(), rtol=0, atol=2e-6)
+    got = selective_scan_backward(x["dout"], dhl, inter, x["D"])
+    ref = orc.ssm_bwd(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["dout"], x["h_prev"], dhl)
+    for name, t in zip(("du", "ddelta", "dA", "dB", "dC", "dD", "dh_prev"), got):
+        np.testing.assert_allclose(t.numpy(), ref[name], rtol=1e-3, atol=1e-4, err_msg=name)
 
 
 def test_scan_status_queue_reports_finished_failures():

@@ -7,6 +7,7 @@ import torch
 
 from mamba_windows_cuda import SelectiveScanCuda, parallel_scan_fn, workloads
 from mamba_windows_cuda.mamba_cuda import SelectiveScanFn, SelectiveScanFnV2
+from mamba_windows_cuda.selective_scan_cuda_ext import FusedSelectiveScanFunction
 from oracle import oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -35,6 +36,30 @@ def test_v1_v2_functions(dev, fn, dtype):
     np.testing.assert_allclose(_np(out), ro, err_msg="out", **TOL[dtype])
     r = orc.ssm_bwd(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["dout"], None, None, clamp=True)
     for k, name in GRADS:
+        assert leaves[k].grad.dtype == dtype, name
+        np.testing.assert_allclose(_np(leaves[k].grad), r[name], err_msg=name, **TOL[dtype])
+
+
+@pytest.mark.parametrize("lvl", [0, 1])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_fused_selective_scan_function(dev, lvl, dtype):
+    """FusedSelectiveScanFunction.apply(u, delta, A, B, C, D, h_prev, checkpoint_lvl) (the reference's
+    class, selective_scan_cuda_ext.py:562-633) at both checkpoint levels: out, h_last, the six
+    gradients and dh_prev against the float64 oracle, with an upstream gradient on h_last too."""
+    print(f"case FusedSelectiveScanFunction lvl={lvl} dtype={dtype}", flush=True)
+    x = workloads.ssm_inputs(2, 260, 150, dtype=dtype, h_prev=True, seed=33)
+    dhl = (0.5 * torch.randn(2, 150, 16, generator=torch.Generator().manual_seed(34))).to(dtype)
+    names = ("u", "delta", "A", "B", "C", "D", "h_prev")
+    leaves = {k: x[k].to(dev).requires_grad_(True) for k in names}
+    out, h_last = FusedSelectiveScanFunction.apply(*(leaves[k] for k in names), lvl)
+    assert out.dtype == dtype and tuple(h_last.shape) == (2, 150, 16)
+    torch.autograd.backward([out, h_last], [x["dout"].to(dev), dhl.to(dev)])
+    torch.cuda.synchronize()
+    ro, rh = orc.ssm_fwd(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["h_prev"], clamp=True)
+    np.testing.assert_allclose(_np(out), ro, err_msg="out", **TOL[dtype])
+    np.testing.assert_allclose(_np(h_last), rh, err_msg="h_last", **TOL[dtype])
+    r = orc.ssm_bwd(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["dout"], x["h_prev"], dhl, clamp=True)
+    for k, name in GRADS + (("h_prev", "dh_prev"),):
         assert leaves[k].grad.dtype == dtype, name
         np.testing.assert_allclose(_np(leaves[k].grad), r[name], err_msg=name, **TOL[dtype])
 

@@ -5,7 +5,24 @@ transforms (bias, softplus, z gate in any combination), launch plan (states per 
 carry split) and checkpoint level from a fixed seed, so the sweep is the same on every run. It
 crosses the combinations the targeted tests cover one axis at a time: out, h_last and every
 gradient (incl. dh_prev, d(delta_bias), dz) must agree with the oracle to the dtype's tolerance.
+
+Sums over (b, t) -- dA, dD and d(delta_bias) -- can cancel: an element can be the small sum of
+hundreds of terms far larger than itself. Its fp32 rounding error then scales with the sum of the
+terms' magnitudes T, not with the element, whichever order or method sums it (each term already
+carries a few ulps of relative error from the L-step reverse recurrence). test_conditioned_case
+replays the seeded cases of a 20,000-case run whose such elements missed the elementwise bound by up
+to 1.44x, and bounds those three outputs by atol + rtol*|y| + K_COND*eps32*T, T from the oracle
+(float64); every other output there keeps the elementwise bound. Measured on those cases: the HIP
+path's errors are 0.4-1.1 eps32*T on d(delta_bias) and 4-6 eps32*T on dA, and its rms relative
+errors over whole tensors equal those of the reference algorithm run in fp32 torch (0.8-1.7x),
+which itself misses the elementwise bound on one of these elements (case 12612, 1.38x). Every fp32
+case with a bias also checks the kernels' own summation: d(delta_bias) against the exact sum of the
+dΔ elements they output, at the elementwise bound.
+
+MWC_SWEEP_CASES=N (opt-in) adds the N cases after MWC_SWEEP_START (default 1700) of the same
+generator, under the same conditioning-aware bound for the three (b, t) sums.
 """
+import os
 import random
 
 import numpy as np
@@ -23,6 +40,12 @@ GRADS = (("u", "du"), ("delta", "ddelta"), ("A", "dA"), ("B", "dB"), ("C", "dC")
 # states per lane built for each state count
 SPLS = {8: (1, 2), 16: (1, 2, 4), 32: (2, 4), 64: (4,)}
 NCASES = 200
+# cases of the 20,000-case run (indices 1700-21699) with a (b, t) sum outside the elementwise bound
+CONDITIONED = (3563, 3938, 12612, 16130, 16997, 20645, 21197)
+K_COND = 4
+EPS32 = 2.0 ** -24
+SWEEP_START = int(os.environ.get("MWC_SWEEP_START", "1700"))
+SWEEP_CASES = int(os.environ.get("MWC_SWEEP_CASES", "0"))
 
 
 def _case(idx):
@@ -36,12 +59,20 @@ def _case(idx):
         lvl=r.choice((0, 0, 1)), seed=r.randint(0, 10 ** 6))
 
 
-def _close(name, got, ref, dtype):
-    np.testing.assert_allclose(got.detach().cpu().double().numpy(), ref, err_msg=name, **TOL[dtype])
+def _close(name, got, ref, dtype, terms=None):
+    """|got - ref| <= atol + rtol*|ref| (+ K_COND*eps32*terms for a (b, t) sum whose terms' magnitude
+    sum is given)."""
+    got = got.detach().cpu().double().numpy()
+    if terms is None:
+        np.testing.assert_allclose(got, ref, err_msg=name, **TOL[dtype])
+        return
+    tol = TOL[dtype]["atol"] + TOL[dtype]["rtol"] * np.abs(ref) + K_COND * EPS32 * terms
+    bad = np.abs(got - ref) > tol
+    assert not bad.any(), (f"{name}: {int(bad.sum())} of {bad.size} elements outside atol + rtol*|y| + "
+                           f"{K_COND}*eps32*T; worst |err|/bound {float((np.abs(got - ref) / tol).max()):.3f}")
 
 
-@pytest.mark.parametrize("idx", range(NCASES))
-def test_random_case(dev, monkeypatch, idx):
+def _run_case(dev, monkeypatch, idx, conditioned):
     c = _case(idx)
     print(f"case random idx={idx} {c}", flush=True)
     for var, key in (("MWC_SPL", "spl"), ("MWC_NSEG", "nseg"), ("MWC_CFOLD", "cfold")):
@@ -75,11 +106,32 @@ def test_random_case(dev, monkeypatch, idx):
     _close("out", out, ro, dtype)
     _close("h_last", h_last, rh, dtype)
     r = orc.ssm_bwd_xf(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["dout"], hp, x["dh_last"], **kw)
+    cond = {"dA": r["dA_abs"], "dD": r["dD_abs"], "ddelta_bias": r["ddelta_bias_abs"]} if conditioned else {}
     for k, name in GRADS:
-        _close(name, leaves[k].grad, r[name], dtype)
+        _close(name, leaves[k].grad, r[name], dtype, cond.get(name))
     if c["with_h"]:
         _close("dh_prev", leaves["h_prev"].grad, r["dh_prev"], dtype)
     if c["bias"]:
-        _close("ddelta_bias", leaves["delta_bias"].grad, r["ddelta_bias"], dtype)
+        _close("ddelta_bias", leaves["delta_bias"].grad, r["ddelta_bias"], dtype, cond.get("ddelta_bias"))
+        if dtype == torch.float32:
+            # the kernels' own summation: d(delta_bias) against the exact (float64) sum of the dΔ elements
+            # they output, at the elementwise bound (so a miss above comes from the terms, not the sum)
+            own = leaves["delta"].grad.double().sum((0, 1)).cpu().numpy()
+            _close("ddelta_bias (sum of own dΔ)", leaves["delta_bias"].grad, own, dtype)
     if c["gate"]:
         _close("dz", leaves["z"].grad, r["dz"], dtype)
+
+
+@pytest.mark.parametrize("idx", range(NCASES))
+def test_random_case(dev, monkeypatch, idx):
+    _run_case(dev, monkeypatch, idx, conditioned=False)
+
+
+@pytest.mark.parametrize("idx", CONDITIONED)
+def test_conditioned_case(dev, monkeypatch, idx):
+    _run_case(dev, monkeypatch, idx, conditioned=True)
+
+
+@pytest.mark.parametrize("idx", range(SWEEP_START, SWEEP_START + SWEEP_CASES))
+def test_sweep_case(dev, monkeypatch, idx):
+    _run_case(dev, monkeypatch, idx, conditioned=True)

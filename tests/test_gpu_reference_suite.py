@@ -33,7 +33,8 @@ TOL = {torch.float32: dict(rtol=1e-3, atol=1e-4), torch.float16: dict(rtol=1e-2,
 
 def _inputs(seed, B, L, D, N, dtype, *, delta_val=0.01, h_prev="zeros"):
     """The reference tests' distributions: u, B, C ~ 0.1 N(0,1); delta constant; A = -0.1 U(0,1);
-    D_ssm = 0.1; h_prev zeros, N(0,1) or absent."""
+    D_ssm = 0.1; h_prev zeros, N(0,1) or absent. (test_gradient_numerical_accuracy redraws u
+    as N(0,1), as the reference test does.)"""
     torch.manual_seed(seed)
     x = dict(u=torch.randn(B, L, D) * 0.1, delta=torch.ones(B, L, D) * delta_val, A=-torch.rand(D, N) * 0.1,
              B=torch.randn(B, L, N) * 0.1, C=torch.randn(B, L, N) * 0.1, D=torch.ones(D) * 0.1)
@@ -171,6 +172,9 @@ def test_gradient_numerical_accuracy(dev, kernel):
     selective_scan_ref's autograd (fp32, bound 1e-3), and against the oracle's adjoint."""
     print("case reference gradient accuracy", flush=True)
     x = _inputs(123, 1, 128, 32, 16, torch.float32, h_prev=None)
+    # this test draws u unscaled (test_selective_scan.py:341), unlike the others' 0.1 N(0,1)
+    torch.manual_seed(123)
+    x["u"] = torch.randn(1, 128, 32)
     leaves = {k: v.to(dev).requires_grad_(True) for k, v in x.items()}
     out, h_last = kernel.forward_with_state(*_args(leaves))
     (out.sum() + h_last.sum()).backward()

@@ -70,8 +70,10 @@ def test_in_place_equals_out_of_place(dev):
     with torch.no_grad():
         y1, h1 = m.step(*args, xd["h_prev"])
         h = xd["h_prev"].clone()
+        v0 = h._version
         y2, h2 = m.step(*args, h, out_state=h)
     assert h2.data_ptr() == h.data_ptr()
+    assert h._version > v0  # the in-place write is visible to autograd's version check
     assert torch.equal(y1, y2) and torch.equal(h1, h2)
 
 

@@ -120,6 +120,36 @@ def test_bwd_matches_autograd(shape, with_h):
         np.testing.assert_allclose(r["dh_prev"], hpl.grad.numpy(), rtol=1e-10, atol=1e-12)
 
 
+def test_term_magnitudes_match_autograd():
+    """dA_abs = sum_{b,t} |delta*dA_t*h_{t-1}*dL/dh_t| and dD_abs = sum_{b,t} |dout*u|, with dL/dh_t
+    taken from torch autograd (retained gradients of every state of the sequential restatement),
+    and dA_abs = dA exactly when every term is non-negative."""
+    bsz, L, dm, n = 2, 13, 5, 8
+    u, delta, A, B, C, D, hp = _inputs(bsz, L, dm, n, seed=61)
+    dout = torch.randn(u.shape, generator=torch.Generator().manual_seed(62), dtype=F64)
+    h = hp.clone().requires_grad_(True)
+    hs, terms = [], []
+    for t in range(L):  # the sequential recurrence with each state kept for its gradient
+        e = torch.exp(delta[:, t, :, None] * A[None])
+        hn = e * h + (delta[:, t] * u[:, t])[..., None] * B[:, t, None, :]
+        hn.retain_grad()
+        hs.append(hn)
+        terms.append((delta[:, t, :, None] * e * h).detach())
+        h = hn
+    out = torch.stack([(hs[t] * C[:, t, None, :]).sum(-1) for t in range(L)], 1) + D * u
+    (out * dout).sum().backward()
+    brute = sum((terms[t] * hs[t].grad).abs() for t in range(L)).sum(0)
+    r = orc.ssm_bwd(u, delta, A, B, C, D, dout, hp, None)
+    np.testing.assert_allclose(r["dA_abs"], brute.numpy(), rtol=1e-10, atol=1e-14)
+    np.testing.assert_allclose(r["dD_abs"], (dout * u).abs().sum((0, 1)).numpy(), rtol=1e-12)
+    assert (r["dA_abs"] > np.abs(r["dA"]) + 1e-9).any()  # these terms have mixed signs
+    # all-positive terms: u, B, C, dout, h_prev >= 0 make every g, h and term >= 0
+    pos = [x.abs() for x in (u, B, C, dout, hp)]
+    r = orc.ssm_bwd(pos[0], delta, A, pos[1], pos[2], D, pos[3], pos[4], None)
+    np.testing.assert_allclose(r["dA_abs"], r["dA"], rtol=1e-12)
+    np.testing.assert_allclose(r["dD_abs"], r["dD"], rtol=1e-12)
+
+
 @pytest.mark.parametrize("bias,softplus,gate", [(True, True, True), (False, True, False), (True, False, False),
                                                 (False, False, True)])
 def test_transforms_match_autograd(bias, softplus, gate):
