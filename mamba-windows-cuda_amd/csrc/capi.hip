@@ -8,6 +8,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 
@@ -119,9 +120,9 @@ double pass_time(int64_t wgs, int64_t chunks, int cap) {
 
 int cpb_of(int ns, int spl) { return 4 * 64 / (ns / spl); }
 
-// Picks the segment count (and the carry split) minimising the modelled time of
-// carry pass + main pass. caps = workgroups per CU each kernel fits (registers, LDS);
-// carry_rel = cost of a carry-pass chunk relative to a main-pass chunk.
+// Picks the segment count (and the carry split) minimising the modelled time of carry pass + main
+// pass. caps = workgroups per CU each kernel fits (registers, LDS); carry_rel = cost of a carry-pass
+// chunk relative to a main-pass chunk.
 SegPlan plan(const SsmShape& s, bool bwd, int spl, int cap_main, int cap_carry, double carry_rel) {
     const int64_t nck = (s.seqlen + kCkptSteps - 1) / kCkptSteps;
     const int64_t w1 = s.batch * ((s.dim + cpb_of(s.nstate, spl) - 1) / cpb_of(s.nstate, spl));
@@ -162,17 +163,61 @@ size_t carry_bytes(const SsmShape& s, const SegPlan& p) {
     return p.nseg > 1 ? align256((size_t)s.batch * p.ncar * s.dim * s.nstate * sizeof(float)) : 0;
 }
 
+// Small problems at N=16 (an unsplit two-states-per-lane grid fills under 1.5 waves per SIMD). Measured
+// sweeps of every (states per lane, segments, carry split) at B=8, L=2048 and D = 192, 384, 768 (fp16,
+// interleaved event timing) put the fastest plan of each shape, forward and backward alike, at two
+// states per lane with exactly one round of full CUs (segments = cap x CUs / workgroups per segment) and
+// the most carry segments that keep each at least 8 chunks long and the carry grid in one round (the
+// planner's cost model picked shorter segments and finer carry splits there: 8-12% slower). Where two
+// states per lane cannot fill 2.25 workgroups per CU with segments of at least 8 chunks, the cost model
+// above decides, at choose_spl's states per lane.
+constexpr int kMinSegChunks = 8;
+
+bool small_problem(const SsmShape& s) {
+    return s.nstate == 16 && s.batch * ((s.dim + cpb_of(16, 2) - 1) / cpb_of(16, 2)) < (int64_t)kCUs * 3 / 2;
+}
+
+// The one-round plan at `spl` states per lane, or nseg = 0 when it does not fill the chip
+SegPlan fill_plan(const SsmShape& s, bool bwd, int spl, int cap_main, int cap_carry) {
+    const int64_t nck = (s.seqlen + kCkptSteps - 1) / kCkptSteps;
+    const int64_t w1 = s.batch * ((s.dim + cpb_of(s.nstate, spl) - 1) / cpb_of(s.nstate, spl));
+    int64_t n = std::min<int64_t>((int64_t)kCUs * cap_main / w1, nck / kMinSegChunks);
+    if (n < 2 || w1 * n * 4 < (int64_t)kCUs * cap_main * 3) return SegPlan{spl, 0, 0, 0, 0};
+    for (int f = 8; f >= 1; f /= 2) {
+        const int64_t cps = ((nck + n - 1) / n + f - 1) / f * f;
+        const int64_t nseg = (nck + cps - 1) / cps;
+        const int64_t ccps = cps / f;
+        const int64_t ncar = bwd ? (nck - cps + ccps - 1) / ccps : (nseg - 1) * f;
+        if (nseg < 2) continue;
+        if (f > 1 && (ccps < kMinSegChunks || w1 * ncar > (int64_t)kCUs * cap_carry)) continue;
+        return SegPlan{spl, (int)nseg, (int)cps, f, (int)ncar};
+    }
+    return SegPlan{spl, 0, 0, 0, 0};
+}
+
+SegPlan plan_dir(const SsmShape& s, bool bwd) {
+    auto caps = [&](int spl, int& cm, int& cc) {
+        cm = bwd ? bwd_cap(s.nstate, spl) : fwd_cap(s.nstate, spl);
+        cc = bwd ? bwd_carry_cap(s.nstate, spl) : fwd_carry_cap(s.nstate, spl);
+    };
+    int cm = 0, cc = 0;
+    const int o = spl_override();
+    const bool forced = env_int("MWC_NSEG", 1, 1 << 20) || env_int("MWC_CFOLD", 1, 64);
+    if (small_problem(s) && !forced && (o == 0 || o == 2)) {
+        caps(2, cm, cc);
+        const SegPlan p = fill_plan(s, bwd, 2, cm, cc);
+        if (p.nseg > 0) return p;
+    }
+    const int spl = choose_spl(s.batch * s.dim, s.nstate);
+    caps(spl, cm, cc);
+    return plan(s, bwd, spl, cm, cc, bwd ? 0.3 : 0.75);
+}
+
 }  // namespace
 
-SegPlan plan_fwd(const SsmShape& s) {
-    const int spl = choose_spl(s.batch * s.dim, s.nstate);
-    return plan(s, false, spl, fwd_cap(s.nstate, spl), fwd_carry_cap(s.nstate, spl), 0.75);
-}
+SegPlan plan_fwd(const SsmShape& s) { return plan_dir(s, false); }
 
-SegPlan plan_bwd(const SsmShape& s) {
-    const int spl = choose_spl(s.batch * s.dim, s.nstate);
-    return plan(s, true, spl, bwd_cap(s.nstate, spl), bwd_carry_cap(s.nstate, spl), 0.3);
-}
+SegPlan plan_bwd(const SsmShape& s) { return plan_dir(s, true); }
 
 size_t fwd_workspace_bytes(const SsmShape& s) {
     // the segment carries when L is split
