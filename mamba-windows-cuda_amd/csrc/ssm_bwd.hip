@@ -807,18 +807,17 @@ __global__ void __launch_bounds__(256) bwd_finish_kernel(const float* __restrict
     }
     const int64_t i = (int64_t)(blockIdx.x - nblk_bc) * 256 + threadIdx.x;
     const int64_t nA = (int64_t)D * NS;
-    // sum of rows 0..nrows-1 in order; eight loads are in flight before their adds
+    // sum of rows 0..nrows-1 in order. Few threads do this part (D*NS of them), so it is latency-bound:
+    // 32 loads are in flight before their adds (rows past nrows add 0, which leaves the sum unchanged).
     auto rows_sum = [nrows](const float* p, int64_t stride) {
         float s = 0.f;
-        int r = 0;
-        for (; r + 8 <= nrows; r += 8) {
-            float v[8];
+        for (int r = 0; r < nrows; r += 32) {
+            float v[32];
 #pragma unroll
-            for (int q = 0; q < 8; ++q) v[q] = p[(int64_t)(r + q) * stride];
+            for (int q = 0; q < 32; ++q) v[q] = r + q < nrows ? p[(int64_t)(r + q) * stride] : 0.f;
 #pragma unroll
-            for (int q = 0; q < 8; ++q) s += v[q];
+            for (int q = 0; q < 32; ++q) s += v[q];
         }
-        for (; r < nrows; ++r) s += p[(int64_t)r * stride];
         return s;
     };
     if (i < nA) {
