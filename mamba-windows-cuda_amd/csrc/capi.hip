@@ -181,6 +181,7 @@ bool small_problem(const SsmShape& s) {
 SegPlan fill_plan(const SsmShape& s, bool bwd, int spl, int cap_main, int cap_carry) {
     const int64_t nck = (s.seqlen + kCkptSteps - 1) / kCkptSteps;
     const int64_t w1 = s.batch * ((s.dim + cpb_of(s.nstate, spl) - 1) / cpb_of(s.nstate, spl));
+    if (w1 <= 0) return SegPlan{spl, 0, 0, 0, 0};  // nothing to launch (empty batch or channels)
     int64_t n = std::min<int64_t>((int64_t)kCUs * cap_main / w1, nck / kMinSegChunks);
     if (n < 2 || w1 * n * 4 < (int64_t)kCUs * cap_main * 3) return SegPlan{spl, 0, 0, 0, 0};
     for (int f = 8; f >= 1; f /= 2) {

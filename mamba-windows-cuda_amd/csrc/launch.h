@@ -17,12 +17,13 @@ bool lane_group_supported(int ns, int spl);
 
 // Waves per SIMD the lane-group kernels are compiled to fit (each lane then has 512/W VGPRs). The
 // forward at four states per lane fits three waves without transforms and two with them.
+// At N=8 and two states per lane a loader thread holds 4 steps of each staged operand (twice N=16's):
+// the carry passes get 5 waves per SIMD instead of 6, which keeps them from spilling at no measured
+// cost. The backward main kernel keeps 3 waves and spills 20-96 bytes per lane there: at 2 waves it
+// does not spill but takes 27% longer (B=8, L=2048, D=1536, N=8: 203.6 against 160.0 us per call).
 constexpr int fwd_min_waves(int spl) { return spl == 4 ? 2 : spl == 1 ? 6 : 3; }
-constexpr int bwd_min_waves(int spl) { return spl == 4 ? 1 : 3; }
-#ifndef MWC_CARRY_WAVES
-#define MWC_CARRY_WAVES 6
-#endif
-constexpr int carry_min_waves(int spl) { return spl == 4 ? 1 : MWC_CARRY_WAVES; }
+constexpr int bwd_min_waves(int ns, int spl) { return spl == 4 ? 1 : 3; }
+constexpr int carry_min_waves(int ns, int spl) { return spl == 4 ? 1 : (ns == 8 && spl == 2) ? 5 : 6; }
 
 // Launch plan of the lane-group kernels: SPL = states held per lane (16/SPL lanes per channel),
 // nseg = segments L is cut into (cps chunks of kCkptSteps steps each), cfold = carry segments per

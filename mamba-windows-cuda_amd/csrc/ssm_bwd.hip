@@ -100,7 +100,7 @@ __device__ __forceinline__ void wave_lds_fence() {
 // segment from g = 0, car_x = its summed base-2 decay exponents (so it maps an
 // adjoint g arriving from its right to 2^car_x * g + car_g).
 template <typename T, int NS, int SPL, int XF>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(carry_min_waves(SPL), 8)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(carry_min_waves(NS, SPL), 8)))
 ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const T* __restrict__ Cm,
                      const T* __restrict__ dout, float* __restrict__ car_g, float* __restrict__ car_x, int Bsz,
                      int L, int D, int nck, int nblk_d, int ncar, int first, int cps, ScanXf xf) {
@@ -291,7 +291,7 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
 
 // XF: the transforms of ScanXf compiled in (kXfDelta, kXfGate bits).
 template <typename T, int NS, int SPL, int XF>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_min_waves(SPL), 8)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_min_waves(NS, SPL), 8)))
 ssm_bwd_kernel(
     const T* __restrict__ u, const T* __restrict__ delta, const T* __restrict__ A, const T* __restrict__ Bm,
     const T* __restrict__ Cm, const T* __restrict__ Dv, const T* __restrict__ dout, const T* __restrict__ dh_last,

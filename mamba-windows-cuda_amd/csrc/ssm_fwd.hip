@@ -76,7 +76,7 @@ enum FwdMode { kMain = 0, kState = 1, kCarry = 2 };
 
 // XF: the transforms of ScanXf compiled in (kXfDelta, kXfGate bits; the gate only with an output).
 template <typename T, int NS, int SPL, int MODE, int XF>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == 2 ? carry_min_waves(SPL) : fwd_min_waves(SPL), 8)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == 2 ? carry_min_waves(NS, SPL) : fwd_min_waves(SPL), 8)))
 ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __restrict__ A,
                const T* __restrict__ Bm, const T* __restrict__ Cm, const T* __restrict__ Dv,
                const T* __restrict__ h_prev, T* __restrict__ out, T* __restrict__ h_last, float* __restrict__ ckpt,

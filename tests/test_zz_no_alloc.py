@@ -1,7 +1,8 @@
 """mwc_ssm_fwd_noalloc (the forward that allocates nothing, its segment carries in a static
 per-device scratch array) against mwc_ssm_fwd_ex with a caller workspace, through the C ABI:
-bitwise-equal outputs on two calls in a row, the second smaller, with L split into segments so that
-the scratch is used; and the size limit."""
+bitwise-equal outputs on calls in a row, each smaller than the one before, with L split into segments
+so that the scratch is used -- the planner's own plan at a small-problem shape, forced plans at one and
+two states per lane, N=8 at two states per lane; and the size limit."""
 import ctypes
 
 import pytest
@@ -14,25 +15,25 @@ def _p(t):
     return None if t is None else t.data_ptr()
 
 
-def _fwd_both(dev, B, L, D, dtype, *, xf, seed):
+def _fwd_both(dev, B, L, D, dtype, *, xf, seed, n=16):
     x = {k: v.to(dev) for k, v in workloads.ssm_inputs(B, L, D, dtype=dtype, h_prev=True, dout=False,
-                                                       seed=seed).items()}
+                                                       seed=seed, nstate=n).items()}
     bias = (0.3 * torch.randn(D, generator=torch.Generator().manual_seed(seed))).to(dtype).to(dev) if xf else None
     z = torch.randn(B, L, D, generator=torch.Generator().manual_seed(seed + 1)).to(dtype).to(dev) if xf else None
     L_ = _lib.lib()
-    nbytes = L_.mwc_ssm_fwd_workspace_size(B, L, D, 16)
+    nbytes = L_.mwc_ssm_fwd_workspace_size(B, L, D, n)
     assert 0 < nbytes <= _lib.NOALLOC_SCRATCH_BYTES  # L is split: the scratch is in use
     nck = L_.mwc_ssm_ckpt_count(L)
     results = []
     for which in ("ex", "noalloc"):
         out = torch.full_like(x["u"], float("nan"))
         out_z = torch.full_like(x["u"], float("nan")) if xf else None
-        h_last = torch.full((B, D, 16), float("nan"), dtype=dtype, device=dev)
-        ckpt = torch.full((B, nck, D, 16), float("nan"), dtype=torch.float32, device=dev)
+        h_last = torch.full((B, D, n), float("nan"), dtype=dtype, device=dev)
+        ckpt = torch.full((B, nck, D, n), float("nan"), dtype=torch.float32, device=dev)
         args = (ops._dtype_code(x["u"]), x["u"].data_ptr(), x["delta"].data_ptr(), x["A"].data_ptr(),
                 x["B"].data_ptr(), x["C"].data_ptr(), x["D"].data_ptr(), x["h_prev"].data_ptr(),
                 _p(bias), int(xf), _p(z), out.data_ptr(), _p(out_z), h_last.data_ptr(),
-                ckpt.data_ptr(), B, L, D, 16)
+                ckpt.data_ptr(), B, L, D, n)
         if which == "ex":
             ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
             st = L_.mwc_ssm_fwd_ex(*args, ws.data_ptr(), nbytes, ops._stream(x["u"].device))
@@ -44,15 +45,27 @@ def _fwd_both(dev, B, L, D, dtype, *, xf, seed):
     return results
 
 
+# (B, L, D, N, dtype, fused transforms, seed, forced plan): each smaller than the one before
+CASES = (
+    (8, 2048, 192, 16, torch.float16, False, 64, None),            # the planner's plan (16 segments)
+    (4, 600, 700, 16, torch.float16, True, 63, ("3", "2")),        # B*D >= 2048: two states per lane
+    (3, 500, 800, 8, torch.bfloat16, False, 65, ("3", "2")),       # N=8 at two states per lane
+    (3, 700, 500, 16, torch.float16, False, 61, ("3", "2")),       # one state per lane
+    (2, 300, 130, 16, torch.float32, True, 62, ("3", "2")),
+)
+
+
 @pytest.mark.gpu
 def test_noalloc_forward_matches_workspace_forward(dev, monkeypatch):
-    monkeypatch.setenv("MWC_NSEG", "3")
-    monkeypatch.setenv("MWC_CFOLD", "2")
-    # two calls in a row on the same GPU (the second smaller, with the fused transforms), each
-    # bitwise equal to the workspace entry point's results
-    for B, L, D, dtype, xf, seed in ((3, 700, 500, torch.float16, False, 61), (2, 300, 130, torch.float32, True, 62)):
-        print(f"case noalloc B={B} L={L} D={D} dtype={dtype} transforms={xf}", flush=True)
-        (o1, z1, h1, c1), (o2, z2, h2, c2) = _fwd_both(dev, B, L, D, dtype, xf=xf, seed=seed)
+    # calls in a row on the same GPU, each bitwise equal to the workspace entry point's results
+    for B, L, D, n, dtype, xf, seed, forced in CASES:
+        print(f"case noalloc B={B} L={L} D={D} N={n} dtype={dtype} transforms={xf} plan={forced}", flush=True)
+        for var, val in zip(("MWC_NSEG", "MWC_CFOLD"), forced or (None, None)):
+            if val is None:
+                monkeypatch.delenv(var, raising=False)
+            else:
+                monkeypatch.setenv(var, val)
+        (o1, z1, h1, c1), (o2, z2, h2, c2) = _fwd_both(dev, B, L, D, dtype, xf=xf, seed=seed, n=n)
         assert torch.isfinite(o1).all() and torch.isfinite(h1).all() and torch.isfinite(c1).all()
         assert torch.equal(o1, o2) and torch.equal(h1, h2) and torch.equal(c1, c2)
         if xf:
