@@ -646,6 +646,25 @@ def summarize(out, dest=None):
                 if nstate_steps:
                     L.append(f"main_kernel_valu_instructions_per_state_step: "
                              f"{sq['SQ_INSTS_VALU'] * 64 / nstate_steps:.3f}")
+            # the call's other kernels: issue use of the carry passes (at cfg2 they scan half of L) and the
+            # finishing kernel's bytes against its traced duration
+            durs = {r["Name"]: float(r["AverageNs"]) for r in _csv_rows(os.path.join(out, "trace_cfg2_fwd_bwd"),
+                                                                      "kernel_stats.csv")}
+            for k in sorted(set(ks) - set(mains[:1])):
+                sq = dict(S1.get(k, {}))
+                sq.update(S2.get(k, {}))
+                kb = F[k]["FETCH_SIZE"] * 1024 * fcal + W.get(k, {}).get("WRITE_SIZE", 0.0) * 1024 * wcal
+                parts = [f"{_short(k)}: {kb:.4g} bytes moved"]
+                if k in durs and durs[k] > 0:
+                    parts.append(f"{kb / durs[k]:.4g} GB/s over its traced {durs[k] / 1e3:.1f} us")
+                wc = sq.get("SQ_WAVE_CYCLES")
+                if wc:
+                    parts.append(f"VALU busy {sq['SQ_ACTIVE_INST_VALU'] / wc:.3f} and LDS busy "
+                                 f"{sq['SQ_ACTIVE_INST_LDS'] / wc:.3f} per wave-cycle")
+                if nstate_steps and "carry" in _short(k) and "SQ_INSTS_VALU" in sq:
+                    parts.append(f"{sq['SQ_INSTS_VALU'] * 64 / (nstate_steps / 2):.3f} VALU instructions per "
+                                 f"state-step of the half of L it scans")
+                L.append("; ".join(parts))
             fname = f"{name}_pmc.txt"
             open(os.path.join(dest, fname), "w").write("\n".join(L) + "\n")
             written.append(fname)
