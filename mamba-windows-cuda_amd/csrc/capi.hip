@@ -120,17 +120,23 @@ double pass_time(int64_t wgs, int64_t chunks, int cap) {
 
 int cpb_of(int ns, int spl) { return 4 * 64 / (ns / spl); }
 
+constexpr int kMinSegChunks = 8;  // shortest (carry) segment the fill and partly split plans make
+
 // Picks the segment count (and the carry split) minimising the modelled time of carry pass + main
 // pass. caps = workgroups per CU each kernel fits (registers, LDS); carry_rel = cost of a carry-pass
 // chunk relative to a main-pass chunk.
-SegPlan plan(const SsmShape& s, bool bwd, int spl, int cap_main, int cap_carry, double carry_rel) {
+SegPlan plan(const SsmShape& s, bool bwd, int spl, int cap_main, int cap_carry, double carry_rel,
+             double* t_out = nullptr) {
     const int64_t nck = (s.seqlen + kCkptSteps - 1) / kCkptSteps;
     const int64_t w1 = s.batch * ((s.dim + cpb_of(s.nstate, spl) - 1) / cpb_of(s.nstate, spl));
     SegPlan best{spl, 1, (int)nck, 1, 0};
     double best_t = pass_time(w1, nck, cap_main);
     // MWC_NSEG / MWC_CFOLD force the segment count / carry split (tuning and tests)
     const int force_n = env_int("MWC_NSEG", 1, 1 << 20), force_f = env_int("MWC_CFOLD", 1, 64);
-    if (force_n == 1 || nck < 2) return best;
+    if (force_n == 1 || nck < 2) {
+        if (t_out) *t_out = best_t;
+        return best;
+    }
     const int n_lo = force_n ? force_n : 2, n_hi = force_n ? force_n : 16;
     for (int n = n_lo; n <= n_hi; ++n) {
         // finer carry splits first: they are measured as fast or faster than the model says
@@ -147,7 +153,39 @@ SegPlan plan(const SsmShape& s, bool bwd, int spl, int cap_main, int cap_carry, 
             }
         }
     }
+    if (t_out) *t_out = best_t;
     return best;
+}
+
+// Partly split plan: when an unsplit grid leaves some CUs one workgroup short of their cap (rows between
+// (cap - 1) and cap per CU), split just enough rows into two segments that the grid fills one round:
+// x = cap * CUs - rows split rows, so a CU runs cap - 1 whole rows and one half. The halves finish at
+// half time and the CU then runs cap - 1 workgroups to the end, instead of the busiest CUs running cap
+// whole rows throughout. Only the split rows need carries. `x_forced` (MWC_NSPLIT) sets x for tests;
+// returns nseg = 0 when no such plan applies. *t_out receives the modelled time.
+SegPlan split_plan(const SsmShape& s, bool bwd, int spl, int cap_main, int cap_carry, double carry_rel, int x_forced,
+                   double* t_out) {
+    const int64_t nck = (s.seqlen + kCkptSteps - 1) / kCkptSteps;
+    const int64_t rows = s.batch * ((s.dim + cpb_of(s.nstate, spl) - 1) / cpb_of(s.nstate, spl));
+    const int64_t slots = (int64_t)kCUs * cap_main;
+    const int64_t x = x_forced > 0 ? x_forced : slots - rows;
+    const SegPlan none{spl, 0, 0, 0, 0};
+    if (nck < 2 || x < 1 || x >= rows) return none;
+    if (x_forced <= 0 && (rows <= slots - kCUs || 2 * rows - slots > (int64_t)kCUs * (cap_main - 1))) return none;
+    for (int f = 8; f >= 1; f /= 2) {
+        const int64_t cps = ((nck + 1) / 2 + f - 1) / f * f;
+        const int64_t ccps = cps / f;
+        if ((nck + cps - 1) / cps != 2) continue;
+        if (f > 1 && (ccps < kMinSegChunks || x * f > (int64_t)kCUs * cap_carry)) continue;
+        const int64_t ncar = bwd ? (nck - cps + ccps - 1) / ccps : f;
+        // a CU with cap - 1 whole rows and one half: all cap run until the half ends, then cap - 1
+        const double t = (double)cps * cap_main / simd_throughput(cap_main) +
+                         (double)(nck - cps) * (cap_main - 1) / simd_throughput(cap_main - 1) + 1.0 +
+                         carry_rel * pass_time(x * ncar, ccps, cap_carry);
+        if (t_out) *t_out = t;
+        return SegPlan{spl, 2, (int)cps, f, (int)ncar, (int)(rows - x)};
+    }
+    return none;
 }
 
 // Workgroups per CU each kernel fits: the runtime's occupancy query for the instance (registers and LDS
@@ -171,8 +209,6 @@ size_t carry_bytes(const SsmShape& s, const SegPlan& p) {
 // planner's cost model picked shorter segments and finer carry splits there: 8-12% slower). Where two
 // states per lane cannot fill 2.25 workgroups per CU with segments of at least 8 chunks, the cost model
 // above decides, at choose_spl's states per lane.
-constexpr int kMinSegChunks = 8;
-
 bool small_problem(const SsmShape& s) {
     return s.nstate == 16 && s.batch * ((s.dim + cpb_of(16, 2) - 1) / cpb_of(16, 2)) < (int64_t)kCUs * 3 / 2;
 }
@@ -211,7 +247,14 @@ SegPlan plan_dir(const SsmShape& s, bool bwd) {
     }
     const int spl = choose_spl(s.batch * s.dim, s.nstate);
     caps(spl, cm, cc);
-    return plan(s, bwd, spl, cm, cc, bwd ? 0.3 : 0.75);
+    const double rel = bwd ? 0.3 : 0.75;
+    const char* e = getenv("MWC_NSPLIT");
+    const int x_forced = e ? atoi(e) : -1;  // MWC_NSPLIT=0 turns partly split plans off
+    double t = 0.0, th = 0.0;
+    const SegPlan p = plan(s, bwd, spl, cm, cc, rel, &t);
+    if (x_forced == 0 || (forced && x_forced < 0) || (p.nseg > 1 && x_forced < 0)) return p;
+    const SegPlan h = split_plan(s, bwd, spl, cm, cc, rel, x_forced, &th);
+    return h.nseg > 0 && (x_forced > 0 || th < t * 0.98) ? h : p;
 }
 
 }  // namespace
@@ -364,7 +407,8 @@ static int fwd_impl(int dtype, const void* u, const void* delta, const void* A, 
     float* car_h = (float*)workspace;
     float* car_x = (float*)((char*)workspace + need / 2);
     const mwc::FwdArgs a{u, delta, A, B_ssm, C_ssm, D_ssm, h_prev, out, h_last, ckpt, car_h, car_x,
-                         p.nseg, p.cps, p.cfold, p.ncar, mwc::ScanXf{delta_bias, z, delta_softplus != 0}, out_z};
+                         p.nseg, p.cps, p.cfold, p.ncar, mwc::ScanXf{delta_bias, z, delta_softplus != 0}, out_z,
+                         p.nfull};
     MWC_HIP_TRY(mwc::launch_ssm_fwd(dtype, s.nstate, p.spl, a, s, st));
     return MWC_OK;
 }
@@ -420,7 +464,7 @@ int mwc_ssm_bwd_ex(int dtype, const void* u, const void* delta, const void* A, c
     float* car_x = (float*)w;
     const mwc::BwdArgs a{u, delta, A, B_ssm, C_ssm, D_ssm, dout, dh_last, ckpt, du, ddelta, dh_prev,
                          dA_part, dD_part, dbc_part, car_g, car_x, p.nseg, p.cps, p.cfold, p.ncar,
-                         mwc::ScanXf{delta_bias, z, delta_softplus != 0}, out, dz, dbias_part};
+                         mwc::ScanXf{delta_bias, z, delta_softplus != 0}, out, dz, dbias_part, p.nfull};
     MWC_HIP_TRY(mwc::launch_ssm_bwd(dtype, s.nstate, p.spl, a, s, st));
     MWC_HIP_TRY(mwc::launch_bwd_finish(dtype, s.nstate, dbc_part, dA_part, dD_part, dbias_part, dB, dC, dA, dD,
                                        delta_bias != nullptr ? ddelta_bias : nullptr, ngrp, p.nseg * (int)batch, s,

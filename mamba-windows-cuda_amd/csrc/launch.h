@@ -28,9 +28,39 @@ constexpr int carry_min_waves(int ns, int spl) { return spl == 4 ? 1 : (ns == 8 
 // Launch plan of the lane-group kernels: SPL = states held per lane (16/SPL lanes per channel),
 // nseg = segments L is cut into (cps chunks of kCkptSteps steps each), cfold = carry segments per
 // segment (the carry passes run cps/cfold chunks per workgroup), ncar = carry segments in all.
+// nfull > 0 marks a partly split plan (nseg = 2): the first nfull rows -- a row is one (batch, channel
+// group) -- run whole, the others as two segments with carries.
 struct SegPlan {
     int spl, nseg, cps, cfold, ncar;
+    int nfull = 0;
 };
+
+// A main-pass workgroup's row (b * nblk_d + channel group) and segment. Uniform plans (nfull == 0) are
+// segment-major. In a partly split plan the workgroups are nfull whole rows and two halves of each other
+// row; when the counts allow, each XCD's contiguous share of the grid (see xcd_remap) holds its whole
+// rows first and its halves after them, so that each CU receives whole rows and halves in the same
+// proportion.
+struct WorkItem {
+    int row, seg;
+    bool whole;  // the row runs unsplit in a partly split plan
+};
+__device__ __forceinline__ WorkItem main_item(int lid, int rows, int nfull, int total) {
+    if (nfull <= 0) return WorkItem{lid % rows, lid / rows, false};
+    int h = lid - nfull;  // half index, or negative for a whole row
+    int f = lid;
+    if (nfull % 8 == 0 && total % 8 == 0) {
+        const int per = total / 8, fx = nfull / 8, x = lid / per, i = lid % per;
+        f = x * fx + i;
+        h = i < fx ? -1 : x * ((total - nfull) / 8) + (i - fx);
+    }
+    if (h < 0) return WorkItem{f, 0, true};
+    return WorkItem{nfull + h / 2, h % 2, false};
+}
+// A carry-pass workgroup's row and carry segment: the carries exist for the split rows only.
+__device__ __forceinline__ WorkItem carry_item(int lid, int rows, int nfull) {
+    const int first = nfull > 0 ? nfull : 0, n = rows - first;
+    return WorkItem{first + lid % n, lid / n, false};
+}
 SegPlan plan_fwd(const SsmShape& s);
 SegPlan plan_bwd(const SsmShape& s);
 // Workgroups per CU of a lane-group kernel instance (the HIP runtime's occupancy query, cached), or 0 when
@@ -65,6 +95,7 @@ struct FwdArgs {
     int nseg, cps, cfold, ncar;
     ScanXf xf;
     void* out_z;               // gated output (xf.z != NULL); `out` then receives the ungated one
+    int nfull;                 // rows run whole in a partly split plan (SegPlan::nfull)
 };
 
 struct BwdArgs {
@@ -80,6 +111,7 @@ struct BwdArgs {
     const void* y;             // ungated forward output (xf.z != NULL)
     void* dz;                  // gradient of z (xf.z != NULL)
     float* dbias_part;         // [nseg][batch][dim] delta_bias partials (xf.delta_bias != NULL)
+    int nfull;                 // rows run whole in a partly split plan (SegPlan::nfull)
 };
 
 // Kernel launchers; `dt` is the storage dtype (mwc_dtype). They only enqueue work.

@@ -103,7 +103,7 @@ template <typename T, int NS, int SPL, int XF>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(carry_min_waves(NS, SPL), 8)))
 ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const T* __restrict__ Cm,
                      const T* __restrict__ dout, float* __restrict__ car_g, float* __restrict__ car_x, int Bsz,
-                     int L, int D, int nck, int nblk_d, int ncar, int first, int cps, ScanXf xf) {
+                     int L, int D, int nck, int nblk_d, int ncar, int first, int cps, ScanXf xf, int nfull) {
     constexpr int LPC = NS / SPL;
     constexpr int CPW = 64 / LPC;
     constexpr int CPB = CPW * 4;
@@ -123,10 +123,10 @@ ssm_bwd_carry_kernel(const T* __restrict__ delta, const T* __restrict__ A, const
 
     const int tid = threadIdx.x;
     const int lid = xcd_remap(blockIdx.x, gridDim.x);
-    const int per_seg = nblk_d * Bsz;
-    const int seg = lid / per_seg;
-    const int b = (lid % per_seg) / nblk_d;
-    const int d0 = (lid % nblk_d) * CPB;
+    const WorkItem wi = carry_item(lid, nblk_d * Bsz, nfull);  // carry segment wi.seg of a split row
+    const int seg = wi.seg;
+    const int b = wi.row / nblk_d;
+    const int d0 = (wi.row % nblk_d) * CPB;
     const int k0 = first + seg * cps;
     const int k1 = min(nck, k0 + cps);
 
@@ -299,7 +299,7 @@ ssm_bwd_kernel(
     float* __restrict__ dA_part, float* __restrict__ dD_part, float* __restrict__ dbc_part,
     const float* __restrict__ car_g, const float* __restrict__ car_x, int Bsz, int L, int D, int nck, int nblk_d,
     int nseg, int cps, int ncar, int cfold, ScanXf xf, const T* __restrict__ yb_out, T* __restrict__ dz,
-    float* __restrict__ dbias_part) {
+    float* __restrict__ dbias_part, int nfull) {
     constexpr int LPC = NS / SPL;
     constexpr int CPW = 64 / LPC;
     constexpr int CPB = CPW * 4;
@@ -343,13 +343,13 @@ ssm_bwd_kernel(
 
     const int tid = threadIdx.x;
     const int lid = xcd_remap(blockIdx.x, gridDim.x);
-    const int per_seg = nblk_d * Bsz;
-    const int seg = lid / per_seg;
-    const int b = (lid % per_seg) / nblk_d;
-    const int blk = lid % nblk_d;
+    const WorkItem wi = main_item(lid, nblk_d * Bsz, nfull, gridDim.x);  // segment wi.seg, or the whole row
+    const int seg = wi.seg;
+    const int b = wi.row / nblk_d;
+    const int blk = wi.row % nblk_d;
     const int d0 = blk * CPB;
-    const int k0 = seg * cps;
-    const int k1 = min(nck, k0 + cps);
+    const int k0 = wi.whole ? 0 : seg * cps;
+    const int k1 = wi.whole ? nck : min(nck, k0 + cps);
 
     const int wave = tid >> 6, lane = tid & 63;
     // a wave's CPW channels take the low lane bits (channel lane % CPW, state group lane / CPW), so a
@@ -383,7 +383,7 @@ ssm_bwd_kernel(
         dAacc[j] = 0.f;
     }
 #pragma unroll 4
-    for (int j = ncar - 1; j >= seg * cfold; --j) {  // g -> 2^xsum * g + G of each following carry segment
+    for (int j = ncar - 1; j >= (wi.whole ? ncar : seg * cfold); --j) {  // g -> 2^xsum * g + G of each following carry segment
         const int64_t o = (((int64_t)b * ncar + j) * D + d) * NS + n0;
         float cg[SPL], cx[SPL];
         ldv<SPL>(car_g + o, cg);
@@ -741,6 +741,12 @@ ssm_bwd_kernel(
         }
         const int64_t pr = (int64_t)seg * Bsz + b;  // partial row
         stv<SPL>(dA_part + (pr * D + d) * NS + n0, dAacc);
+        if (wi.whole) {  // a whole row of a partly split plan: its other segments' partial rows are zero
+            float z[SPL];
+#pragma unroll
+            for (int j = 0; j < SPL; ++j) z[j] = 0.f;
+            for (int s2 = 1; s2 < nseg; ++s2) stv<SPL>(dA_part + (((int64_t)s2 * Bsz + b) * D + d) * NS + n0, z);
+        }
     }
     {  // dD (and delta_bias) partials: the NSG loader threads of a channel, in order
         const bool with_bias = XD && xf.delta_bias != nullptr;
@@ -758,6 +764,10 @@ ssm_bwd_kernel(
             }
             dD_part[pr * D + d0 + tid] = acc;
             if (with_bias) dbias_part[pr * D + d0 + tid] = accb;
+            for (int s2 = 1; wi.whole && s2 < nseg; ++s2) {  // as for dA
+                dD_part[((int64_t)s2 * Bsz + b) * D + d0 + tid] = 0.f;
+                if (with_bias) dbias_part[((int64_t)s2 * Bsz + b) * D + d0 + tid] = 0.f;
+            }
         }
     }
 }
@@ -862,17 +872,20 @@ template <typename T, int NS, int SPL, int XF>
 static hipError_t bwd_inst(const BwdArgs& a, const SsmShape& s, hipStream_t st) {
     const int nblk_d = bwd_groups(s, NS, SPL);
     const int nck = (int)((s.seqlen + kCkptSteps - 1) / kCkptSteps);
-    const int per_seg = nblk_d * (int)s.batch;
+    // a partly split plan launches its whole rows once and its split rows once per (carry) segment
+    const int rows = nblk_d * (int)s.batch, split = a.nfull > 0 ? rows - a.nfull : rows;
     if (a.nseg > 1)  // carries of every chunk after the first segment
-        hipLaunchKernelGGL((ssm_bwd_carry_kernel<T, NS, SPL, XF>), dim3(per_seg * a.ncar), dim3(256), 0, st,
+        hipLaunchKernelGGL((ssm_bwd_carry_kernel<T, NS, SPL, XF>), dim3(split * a.ncar), dim3(256), 0, st,
                            (const T*)a.delta, (const T*)a.A, (const T*)a.C, (const T*)a.dout, a.car_g, a.car_x,
                            (int)s.batch, (int)s.seqlen, (int)s.dim, nck, nblk_d, a.ncar, a.cps, a.cps / a.cfold,
-                           a.xf);
-    hipLaunchKernelGGL((ssm_bwd_kernel<T, NS, SPL, XF>), dim3(per_seg * a.nseg), dim3(256), 0, st, (const T*)a.u,
+                           a.xf, a.nfull);
+    hipLaunchKernelGGL((ssm_bwd_kernel<T, NS, SPL, XF>), dim3((a.nfull > 0 ? a.nfull : 0) + split * a.nseg),
+                       dim3(256), 0, st, (const T*)a.u,
                        (const T*)a.delta, (const T*)a.A, (const T*)a.B, (const T*)a.C, (const T*)a.Dv,
                        (const T*)a.dout, (const T*)a.dh_last, a.ckpt, (T*)a.du, (T*)a.ddelta, (T*)a.dh_prev,
                        a.dA_part, a.dD_part, a.dbc_part, a.car_g, a.car_x, (int)s.batch, (int)s.seqlen, (int)s.dim,
-                       nck, nblk_d, a.nseg, a.cps, a.ncar, a.cfold, a.xf, (const T*)a.y, (T*)a.dz, a.dbias_part);
+                       nck, nblk_d, a.nseg, a.cps, a.ncar, a.cfold, a.xf, (const T*)a.y, (T*)a.dz, a.dbias_part,
+                       a.nfull);
     return hipGetLastError();
 }
 

@@ -81,7 +81,7 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
                const T* __restrict__ Bm, const T* __restrict__ Cm, const T* __restrict__ Dv,
                const T* __restrict__ h_prev, T* __restrict__ out, T* __restrict__ h_last, float* __restrict__ ckpt,
                float* __restrict__ car_h, float* __restrict__ car_x, int Bsz, int L, int D, int nck, int nblk_d,
-               int nseg, int cps, int ncar, int cfold, ScanXf xf, T* __restrict__ out_z) {
+               int nseg, int cps, int ncar, int cfold, ScanXf xf, T* __restrict__ out_z, int nfull) {
     constexpr bool HAS_OUT = MODE == kMain;
     constexpr bool CARRY = MODE == kCarry;
     constexpr int LPC = NS / SPL;  // lanes per channel
@@ -106,12 +106,13 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
 
     const int tid = threadIdx.x;
     const int lid = xcd_remap(blockIdx.x, gridDim.x);
-    const int per_seg = nblk_d * Bsz;
-    const int seg = lid / per_seg;
-    const int b = (lid % per_seg) / nblk_d;
-    const int d0 = (lid % nblk_d) * CPB;
-    const int k0 = seg * cps;
-    const int k1 = min(nck, k0 + cps);
+    // (the carry pass: carry segment seg of cps chunks; the main pass: segment seg, or the whole row)
+    const WorkItem wi = CARRY ? carry_item(lid, nblk_d * Bsz, nfull) : main_item(lid, nblk_d * Bsz, nfull, gridDim.x);
+    const int seg = wi.seg;
+    const int b = wi.row / nblk_d;
+    const int d0 = (wi.row % nblk_d) * CPB;
+    const int k0 = wi.whole ? 0 : seg * cps;
+    const int k1 = wi.whole ? nck : min(nck, k0 + cps);
 
     // consumer role
     const int wave = tid >> 6, lane = tid & 63;
@@ -371,7 +372,7 @@ ssm_fwd_kernel(const T* __restrict__ u, const T* __restrict__ delta, const T* __
             vst<SPL>(car_h + car0 + seg * car_seg, h);
             vst<SPL>(car_x + car0 + seg * car_seg, xs);
         }
-    } else if (h_last != nullptr && valid && seg == nseg - 1) {
+    } else if (h_last != nullptr && valid && k1 == nck) {  // the row's last segment
 #pragma unroll
         for (int j = 0; j < SPL; ++j) st(h_last + ((int64_t)b * D + d) * NS + n0 + j, h[j]);
     }
@@ -382,12 +383,15 @@ static void fwd_launch(const FwdArgs& a, const SsmShape& s, int nseg_launched, h
     constexpr int CPB = 4 * 64 / (NS / SPL);
     const int nblk_d = (int)((s.dim + CPB - 1) / CPB);
     const int nck = (int)((s.seqlen + kCkptSteps - 1) / kCkptSteps);
-    const int grid = nblk_d * (int)s.batch * nseg_launched;
+    // a partly split plan launches its whole rows once and its split rows once per segment (carry pass: once
+    // per carry segment)
+    const int rows = nblk_d * (int)s.batch, split = a.nfull > 0 ? rows - a.nfull : rows;
+    const int grid = MODE == kCarry ? split * nseg_launched : (a.nfull > 0 ? a.nfull : 0) + split * nseg_launched;
     hipLaunchKernelGGL((ssm_fwd_kernel<T, NS, SPL, MODE, XF>), dim3(grid), dim3(256), 0, st, (const T*)a.u,
                        (const T*)a.delta, (const T*)a.A, (const T*)a.B, (const T*)a.C, (const T*)a.Dv,
                        (const T*)a.h_prev, (T*)a.out, (T*)a.h_last, a.ckpt, a.car_h, a.car_x, (int)s.batch,
                        (int)s.seqlen, (int)s.dim, nck, nblk_d, a.nseg, MODE == kCarry ? a.cps / a.cfold : a.cps,
-                       a.ncar, a.cfold, a.xf, (T*)a.out_z);
+                       a.ncar, a.cfold, a.xf, (T*)a.out_z, a.nfull);
 }
 
 template <typename T, int NS, int SPL, int XF>

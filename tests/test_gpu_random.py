@@ -72,11 +72,35 @@ def _close(name, got, ref, dtype, terms=None):
                            f"{K_COND}*eps32*T; worst |err|/bound {float((np.abs(got - ref) / tol).max()):.3f}")
 
 
-def _run_case(dev, monkeypatch, idx, conditioned):
+def _split_case(idx):
+    """A case run with a partly split plan (MWC_NSPLIT): some rows whole, the others as two segments.
+    Sizes make the grid's whole-row and half counts multiples of 8 in about half of the cases, which
+    takes the XCD-balanced work mapping. fp32 cases keep the sweep's lengths (at most 260 steps);
+    fp16/bf16 cases run 260-900 steps, long enough to split the carries. (At longer L some fp32 dΔ
+    elements are so ill-conditioned -- 1e-3 from terms summing to 80 in magnitude -- that fp32
+    rounding exceeds the elementwise bound under every plan, split or not.)"""
+    r = random.Random(5100 + idx)
     c = _case(idx)
+    spl = r.choice((1, 2))
+    L = r.randint(40, 260) if c["dtype"] == torch.float32 else r.randint(260, 900)
+    c.update(n=16, spl=spl, nseg=None, cfold=None, lvl=r.choice((0, 1)), L=L)
+    cpb = 16 * spl
+    if r.random() < 0.5:  # rows and the split count multiples of 8
+        c["B"] = r.choice((1, 2, 4))
+        c["D"] = cpb * 8 // c["B"] * r.randint(1, 2) - r.randint(0, cpb - 1)
+        rows = c["B"] * -(-c["D"] // cpb)
+        c["nsplit"] = 8 * r.randint(1, rows // 8 - 1) if rows >= 16 else r.randint(1, rows - 1)
+    else:
+        rows = c["B"] * -(-c["D"] // cpb)
+        c["nsplit"] = r.randint(1, max(1, rows - 1))
+    return c
+
+
+def _run_case(dev, monkeypatch, idx, conditioned, c=None):
+    c = c or _case(idx)
     print(f"case random idx={idx} {c}", flush=True)
-    for var, key in (("MWC_SPL", "spl"), ("MWC_NSEG", "nseg"), ("MWC_CFOLD", "cfold")):
-        if c[key] is not None:
+    for var, key in (("MWC_SPL", "spl"), ("MWC_NSEG", "nseg"), ("MWC_CFOLD", "cfold"), ("MWC_NSPLIT", "nsplit")):
+        if c.get(key) is not None:
             monkeypatch.setenv(var, str(c[key]))
     B, L, D, n, dtype = c["B"], c["L"], c["D"], c["n"], c["dtype"]
     x = workloads.ssm_inputs(B, L, D, dtype=torch.float32, h_prev=True, seed=c["seed"], nstate=n)
@@ -125,6 +149,11 @@ def _run_case(dev, monkeypatch, idx, conditioned):
 @pytest.mark.parametrize("idx", range(NCASES))
 def test_random_case(dev, monkeypatch, idx):
     _run_case(dev, monkeypatch, idx, conditioned=False)
+
+
+@pytest.mark.parametrize("idx", range(40))
+def test_partly_split_case(dev, monkeypatch, idx):
+    _run_case(dev, monkeypatch, idx, conditioned=False, c=_split_case(idx))
 
 
 @pytest.mark.parametrize("idx", CONDITIONED)
