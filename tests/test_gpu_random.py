@@ -72,19 +72,20 @@ def _close(name, got, ref, dtype, terms=None):
                            f"{K_COND}*eps32*T; worst |err|/bound {float((np.abs(got - ref) / tol).max()):.3f}")
 
 
-def _split_case(idx):
+def _split_case(idx, n=16):
     """A case run with a partly split plan (MWC_NSPLIT): some rows whole, the others as two segments.
     Sizes make the grid's whole-row and half counts multiples of 8 in about half of the cases, which
     takes the XCD-balanced work mapping. fp32 cases keep the sweep's lengths (at most 260 steps);
     fp16/bf16 cases run 260-900 steps, long enough to split the carries. (At longer L some fp32 dΔ
     elements are so ill-conditioned -- 1e-3 from terms summing to 80 in magnitude -- that fp32
-    rounding exceeds the elementwise bound under every plan, split or not.)"""
-    r = random.Random(5100 + idx)
+    rounding exceeds the elementwise bound under every plan, split or not.) N=16 cases take one or
+    two states per lane; the other state counts take any built lane group."""
+    r = random.Random((5100 if n == 16 else 5300 + 100 * n) + idx)
     c = _case(idx)
-    spl = r.choice((1, 2))
+    spl = r.choice((1, 2) if n == 16 else SPLS[n])
     L = r.randint(40, 260) if c["dtype"] == torch.float32 else r.randint(260, 900)
-    c.update(n=16, spl=spl, nseg=None, cfold=None, lvl=r.choice((0, 1)), L=L)
-    cpb = 16 * spl
+    c.update(n=n, spl=spl, nseg=None, cfold=None, lvl=r.choice((0, 1)), L=L)
+    cpb = 256 * spl // n  # channels per workgroup
     if r.random() < 0.5:  # rows and the split count multiples of 8
         c["B"] = r.choice((1, 2, 4))
         c["D"] = cpb * 8 // c["B"] * r.randint(1, 2) - r.randint(0, cpb - 1)
@@ -154,6 +155,12 @@ def test_random_case(dev, monkeypatch, idx):
 @pytest.mark.parametrize("idx", range(40))
 def test_partly_split_case(dev, monkeypatch, idx):
     _run_case(dev, monkeypatch, idx, conditioned=False, c=_split_case(idx))
+
+
+@pytest.mark.parametrize("n", (8, 32, 64))
+@pytest.mark.parametrize("idx", range(6))
+def test_partly_split_nstate_case(dev, monkeypatch, n, idx):
+    _run_case(dev, monkeypatch, idx, conditioned=False, c=_split_case(idx, n))
 
 
 @pytest.mark.parametrize("idx", CONDITIONED)
