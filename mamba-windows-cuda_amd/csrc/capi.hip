@@ -1,9 +1,10 @@
 // extern "C" entry points declared in include/mwc_ssm.h.
 //
 // Argument validation restates the reference host wrappers' contract
-// (mamba_cuda.py:185-238, 281-326): N must be 16, dtypes fp32/fp16, shapes
-// consistent. Everything is checked before the first launch; the functions
-// only enqueue work on the caller's stream and never allocate.
+// (mamba_cuda.py:185-238, 281-326: N = 16, fp32/fp16, consistent shapes), widened
+// to N = 8, 32, 64 and bf16 storage. Everything is checked before the first
+// launch; the functions only enqueue work on the caller's stream and never
+// allocate.
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
