@@ -48,7 +48,7 @@ def _load():
         I = ctypes.c_int64
         lib.oracle_ssm_fwd.argtypes = [I, I, I, I, P, P, P, P, P, P, P, ctypes.c_int, P, P]
         lib.oracle_ssm_bwd.argtypes = [I, I, I, I, P, P, P, P, P, P, P, P, P, ctypes.c_int,
-                                       P, P, P, P, P, P, P, P]
+                                       P, P, P, P, P, P, P, P, P, P]
         lib.oracle_pscan_fwd.argtypes = [I, I, I, P, P, P]
         lib.oracle_pscan_bwd.argtypes = [I, I, I, P, P, P, P, P]
         for f in (lib.oracle_ssm_fwd, lib.oracle_ssm_bwd, lib.oracle_pscan_fwd, lib.oracle_pscan_bwd):
@@ -86,21 +86,27 @@ def ssm_fwd(u, delta, A, B, C, D, h_prev=None, clamp=False):
 
 
 def ssm_bwd(u, delta, A, B, C, D, dout, h_prev=None, dh_last=None, clamp=False):
-    """Returns dict du, ddelta, dA, dB, dC, dD, dh_prev (all float64), plus the magnitudes of the
-    terms of the two sums over (b, t): dA_abs = sum |g*delta*dA_t*h_{t-1}| (D,N) and
-    dD_abs = sum |dout*u| (D,) -- the scale of the rounding error an fp32 evaluation of dA and dD
-    carries (conditioning measures for tests)."""
+    """Returns dict du, ddelta, dA, dB, dC, dD, dh_prev (all float64), plus conditioning measures for
+    tests (not gradients): the running-error magnitudes dA_abs (D,N), ddelta_abs and du_abs (B,L,D) --
+    each output's sum with every term replaced by its magnitude and the state h and adjoint
+    g = dL/dh_t by recurrences run on magnitudes (H_t = dA_t H_{t-1} + |delta u B|, H_{-1} = |h_prev|;
+    G_t = |dout_t C_t| + dA_{t+1} G_{t+1}, G_{L-1} including |dh_last|):
+    dA_abs = sum_{b,t} |delta| G dA_t H_{t-1}, ddelta_abs = sum_n |A| G dA_t H_{t-1} + |u| sum_n G |B|,
+    du_abs = |D dout| + |delta| sum_n G |B| -- and dD_abs = sum_{b,t} |dout u| (D,). An fp32 evaluation
+    of an output errs by a few eps32 times its magnitude sum, whatever cancels in h, g or the sum."""
     u, delta, A, B, C, D, dout, h_prev, dh_last = map(
         _f64, (u, delta, A, B, C, D, dout, h_prev, dh_last))
     Bsz, L, Dm = u.shape
     N = A.shape[1]
     r = dict(du=np.empty((Bsz, L, Dm)), ddelta=np.empty((Bsz, L, Dm)), dA=np.empty((Dm, N)),
              dB=np.empty((Bsz, L, N)), dC=np.empty((Bsz, L, N)), dD=np.empty((Dm,)),
-             dh_prev=np.empty((Bsz, Dm, N)), dA_abs=np.empty((Dm, N)))
+             dh_prev=np.empty((Bsz, Dm, N)), dA_abs=np.empty((Dm, N)), ddelta_abs=np.empty((Bsz, L, Dm)),
+             du_abs=np.empty((Bsz, L, Dm)))
     _load().oracle_ssm_bwd(Bsz, L, Dm, N, _p(u), _p(delta), _p(A), _p(B), _p(C), _p(D),
                            _p(h_prev), _p(dout), _p(dh_last), int(bool(clamp)),
                            _p(r["du"]), _p(r["ddelta"]), _p(r["dA"]), _p(r["dB"]), _p(r["dC"]),
-                           _p(r["dD"]), _p(r["dh_prev"]), _p(r["dA_abs"]))
+                           _p(r["dD"]), _p(r["dh_prev"]), _p(r["dA_abs"]), _p(r["ddelta_abs"]),
+                           _p(r["du_abs"]))
     r["dD_abs"] = np.abs(dout * u).sum(axis=(0, 1))
     return r
 
@@ -132,9 +138,9 @@ def ssm_fwd_xf(u, delta, A, B, C, D, h_prev=None, delta_bias=None, delta_softplu
 
 def ssm_bwd_xf(u, delta, A, B, C, D, dout, h_prev=None, dh_last=None, delta_bias=None, delta_softplus=False,
                z=None, clamp=False):
-    """ssm_bwd through the transforms. Returns the ssm_bwd dict (ddelta w.r.t. the raw delta) plus
-    'ddelta_bias', its terms' magnitude sum 'ddelta_bias_abs' = sum_{b,t} |ddelta|, and 'dz' (None
-    when the transform is absent)."""
+    """ssm_bwd through the transforms. Returns the ssm_bwd dict (ddelta and ddelta_abs w.r.t. the raw
+    delta) plus 'ddelta_bias', its magnitude sum 'ddelta_bias_abs' = sum_{b,t} ddelta_abs, and 'dz'
+    (None when the transform is absent)."""
     dxf, dpre = _delta_xf(delta, delta_bias, delta_softplus)
     g = _f64(dout)
     dz = None
@@ -147,8 +153,9 @@ def ssm_bwd_xf(u, delta, A, B, C, D, dout, h_prev=None, dh_last=None, delta_bias
     r = ssm_bwd(u, dxf, A, B, C, D, g, h_prev, dh_last, clamp)
     if delta_softplus:
         r["ddelta"] = r["ddelta"] * _sigmoid(dpre)
+        r["ddelta_abs"] = r["ddelta_abs"] * _sigmoid(dpre)
     r["ddelta_bias"] = r["ddelta"].sum(axis=(0, 1)) if delta_bias is not None else None
-    r["ddelta_bias_abs"] = np.abs(r["ddelta"]).sum(axis=(0, 1)) if delta_bias is not None else None
+    r["ddelta_bias_abs"] = r["ddelta_abs"].sum(axis=(0, 1)) if delta_bias is not None else None
     r["dz"] = dz
     return r
 

@@ -21,10 +21,18 @@
  *                         ddelta= sum_n g*(A*dA_t*h_{t-1} + u*B)
  *                         dA    = sum_{b,t} g*delta*dA_t*h_{t-1}
  *                         dD    = sum_{b,t} dout*u        dh_prev = dA_0*g_0
- *                       plus, when dA_abs is not NULL, sum_{b,t} |g*delta*dA_t*h_{t-1}|:
- *                       the sum of dA's terms' magnitudes, the scale of the rounding
- *                       error that any fp32 evaluation of the sum carries (a
- *                       conditioning measure for tests, not a gradient).
+ *                       plus, when not NULL, the running-error magnitudes of dA,
+ *                       ddelta and du (conditioning measures for tests, not
+ *                       gradients): the same sums with every term replaced by its
+ *                       magnitude and h, g by the recurrences run on magnitudes,
+ *                         H_t = dA_t*H_{t-1} + |delta*u*B|,  H_{-1} = |h_prev|
+ *                         G_t = |dout_t*C_t| + dA_{t+1}*G_{t+1}, G_{L-1} incl. |dh_last|
+ *                         dA_abs     = sum_{b,t} |delta|*G*dA_t*H_{t-1}
+ *                         ddelta_abs = sum_n |A|*G*dA_t*H_{t-1} + |u|*sum_n G*|B|
+ *                         du_abs     = |D*dout| + |delta|*sum_n G*|B|
+ *                       (bounds of |h| and |g| free of cancellation: an fp32
+ *                       evaluation's error in each output is a few eps32 times its
+ *                       magnitude sum, whatever the cancellation in h, g or the sum).
  *   oracle_pscan_fwd <- parallel_scan_ref, mamba_windows_cuda/pscan.py:153-171
  *                       (H_0 = X_0, A_0 ignored; H_t = A_t*H_{t-1} + X_t)
  *   oracle_pscan_bwd <- its adjoint: G~_t = dH_t + A_{t+1}*G~_{t+1};
@@ -96,7 +104,7 @@ void oracle_ssm_bwd(i64 Bsz, i64 L, i64 Dm, i64 N, const double* u, const double
                     const double* A, const double* Bm, const double* Cm, const double* Dv,
                     const double* h_prev, const double* dout, const double* dh_last, int clamp,
                     double* du, double* ddelta, double* dA, double* dB, double* dC, double* dD,
-                    double* dh_prev, double* dA_abs) {
+                    double* dh_prev, double* dA_abs, double* ddelta_abs, double* du_abs) {
     const i64 nblk = (Dm + OR_BBLK - 1) / OR_BBLK;
     const i64 nitems = Bsz * nblk;
     /* per-item partials, summed afterwards in item order (deterministic) */
@@ -114,6 +122,9 @@ void oracle_ssm_bwd(i64 Bsz, i64 L, i64 Dm, i64 N, const double* u, const double
         double* eA = (double*)malloc((size_t)L * nd * N * sizeof(double));
         double* g = (double*)malloc((size_t)nd * N * sizeof(double));
         double* hp = (double*)malloc((size_t)nd * N * sizeof(double));
+        /* the magnitude recurrences H, G of the running-error sums */
+        double* hista = (double*)malloc((size_t)L * nd * N * sizeof(double));
+        double* ga = (double*)malloc((size_t)nd * N * sizeof(double));
         for (i64 d = d0; d < d1; ++d)
             for (i64 n = 0; n < N; ++n) hp[(d - d0) * N + n] = h_prev ? h_prev[(b * Dm + d) * N + n] : 0.0;
         for (i64 t = 0; t < L; ++t) {
@@ -127,12 +138,15 @@ void oracle_ssm_bwd(i64 Bsz, i64 L, i64 Dm, i64 N, const double* u, const double
                     const double e = exp(clamp88(dt * A[d * N + n], clamp));
                     eA[(t * nd) * N + k] = e;
                     hist[(t * nd) * N + k] = e * prev + dt * ut * Bt[n];
+                    const double preva = t ? hista[((t - 1) * nd) * N + k] : fabs(hp[k]);
+                    hista[(t * nd) * N + k] = e * preva + fabs(dt * ut * Bt[n]);
                 }
             }
         }
         for (i64 k = 0; k < nd * N; ++k) {
             const i64 d = d0 + k / N, n = k % N;
             g[k] = dh_last ? dh_last[(b * Dm + d) * N + n] : 0.0; /* carried part dA_{t+1} g_{t+1} */
+            ga[k] = fabs(g[k]);
         }
         double* myBC = pBC + (size_t)item * L * N * 2;
         double* myA = pA + (size_t)item * OR_BBLK * N;
@@ -144,7 +158,7 @@ void oracle_ssm_bwd(i64 Bsz, i64 L, i64 Dm, i64 N, const double* u, const double
             const double* Ct = Cm + (b * L + t) * N;
             for (i64 d = d0; d < d1; ++d) {
                 const double dt = delta[row + d], ut = u[row + d], yo = dout[row + d];
-                double r1 = 0.0, r2 = 0.0;
+                double r1 = 0.0, r2 = 0.0, r1a = 0.0, r2a = 0.0;
                 for (i64 n = 0; n < N; ++n) {
                     const i64 k = (d - d0) * N + n;
                     const double ht = hist[(t * nd) * N + k];
@@ -157,11 +171,19 @@ void oracle_ssm_bwd(i64 Bsz, i64 L, i64 Dm, i64 N, const double* u, const double
                     const double s = gt * e * prev;
                     r2 += A[d * N + n] * s;
                     myA[(d - d0) * N + n] += dt * s;
-                    myAa[(d - d0) * N + n] += fabs(dt * s);
                     g[k] = e * gt;
+                    /* magnitudes */
+                    const double gta = ga[k] + fabs(yo * Ct[n]);
+                    const double sa = gta * e * (t ? hista[((t - 1) * nd) * N + k] : fabs(hp[k]));
+                    r1a += gta * fabs(Bt[n]);
+                    r2a += fabs(A[d * N + n]) * sa;
+                    myAa[(d - d0) * N + n] += fabs(dt) * sa;
+                    ga[k] = e * gta;
                 }
                 du[row + d] = Dv[d] * yo + dt * r1;
                 ddelta[row + d] = r2 + ut * r1;
+                if (ddelta_abs) ddelta_abs[row + d] = r2a + fabs(ut) * r1a;
+                if (du_abs) du_abs[row + d] = fabs(Dv[d] * yo) + fabs(dt) * r1a;
                 myD[d - d0] += yo * ut;
             }
         }
@@ -174,6 +196,8 @@ void oracle_ssm_bwd(i64 Bsz, i64 L, i64 Dm, i64 N, const double* u, const double
         free(eA);
         free(g);
         free(hp);
+        free(hista);
+        free(ga);
     }
     /* deterministic reductions */
     for (i64 b = 0; b < Bsz; ++b)

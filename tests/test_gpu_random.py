@@ -6,21 +6,23 @@ carry split) and checkpoint level from a fixed seed, so the sweep is the same on
 crosses the combinations the targeted tests cover one axis at a time: out, h_last and every
 gradient (incl. dh_prev, d(delta_bias), dz) must agree with the oracle to the dtype's tolerance.
 
-Sums over (b, t) -- dA, dD and d(delta_bias) -- can cancel: an element can be the small sum of
-hundreds of terms far larger than itself. Its fp32 rounding error then scales with the sum of the
-terms' magnitudes T, not with the element, whichever order or method sums it (each term already
-carries a few ulps of relative error from the L-step reverse recurrence). test_conditioned_case
-replays the seeded cases of a 20,000-case run whose such elements missed the elementwise bound by up
-to 1.44x, and bounds those three outputs by atol + rtol*|y| + K_COND*eps32*T, T from the oracle
-(float64); every other output there keeps the elementwise bound. Measured on those cases: the HIP
-path's errors are 0.4-1.1 eps32*T on d(delta_bias) and 4-6 eps32*T on dA, and its rms relative
-errors over whole tensors equal those of the reference algorithm run in fp32 torch (0.8-1.7x),
-which itself misses the elementwise bound on one of these elements (case 12612, 1.38x). Every fp32
-case with a bias also checks the kernels' own summation: d(delta_bias) against the exact sum of the
-dΔ elements they output, at the elementwise bound.
+Sums can cancel: an element can be the small sum of terms far larger than itself, and the state h
+and adjoint g that make up the terms can themselves be small sums of larger parts. The fp32 rounding
+error then scales with the output's running-error magnitude T -- its sum with every term replaced by
+its magnitude and h, g by recurrences run on magnitudes (the oracle's dA_abs, ddelta_abs, du_abs,
+dD_abs, ddelta_bias_abs) -- not with the element. That holds for the sums over (b, t) -- dA, dD and
+d(delta_bias) -- and for the sums over the N states inside each dΔ and du element.
+test_conditioned_case replays the seeded sweep cases (indices 1700-21699 and 21700-37855) with such an
+element outside the elementwise bound (by up to 1.44x), and bounds these five outputs by
+atol + rtol*|y| + K_COND*eps32*T; every other output keeps the elementwise bound. Measured on those
+cases: the HIP path's errors stay below 2.9 eps32*T on dA and 4.7 eps32*T on dΔ, under the same
+ratios for the reference algorithm run sequentially in fp32 (3.8 and 7.5), which itself misses the
+elementwise bound on elements of these cases (12612 dA 1.38x, 26676 dΔ 1.22x, 37855 dA). Every fp32
+case with a bias also checks the kernels' own summation: d(delta_bias) against the exact sum of the dΔ
+elements they output, at the elementwise bound.
 
 MWC_SWEEP_CASES=N (opt-in) adds the N cases after MWC_SWEEP_START (default 1700) of the same
-generator, under the same conditioning-aware bound for the three (b, t) sums.
+generator, under the same conditioning-aware bound for those five outputs.
 """
 import os
 import random
@@ -40,8 +42,9 @@ GRADS = (("u", "du"), ("delta", "ddelta"), ("A", "dA"), ("B", "dB"), ("C", "dC")
 # states per lane built for each state count
 SPLS = {8: (1, 2), 16: (1, 2, 4), 32: (2, 4), 64: (4,)}
 NCASES = 200
-# cases of the 20,000-case run (indices 1700-21699) with a (b, t) sum outside the elementwise bound
-CONDITIONED = (3563, 3938, 12612, 16130, 16997, 20645, 21197)
+# sweep cases with an ill-conditioned sum outside the elementwise bound: (b, t) sums in the 20,000
+# cases 1700-21699; a dΔ element (N=64) and a dA element in 21700-37855
+CONDITIONED = (3563, 3938, 12612, 16130, 16997, 20645, 21197, 26676, 37855)
 K_COND = 4
 EPS32 = 2.0 ** -24
 SWEEP_START = int(os.environ.get("MWC_SWEEP_START", "1700"))
@@ -60,8 +63,8 @@ def _case(idx):
 
 
 def _close(name, got, ref, dtype, terms=None):
-    """|got - ref| <= atol + rtol*|ref| (+ K_COND*eps32*terms for a (b, t) sum whose terms' magnitude
-    sum is given)."""
+    """|got - ref| <= atol + rtol*|ref| (+ K_COND*eps32*terms for a sum whose terms' magnitude sum is
+    given)."""
     got = got.detach().cpu().double().numpy()
     if terms is None:
         np.testing.assert_allclose(got, ref, err_msg=name, **TOL[dtype])
@@ -131,7 +134,8 @@ def _run_case(dev, monkeypatch, idx, conditioned, c=None):
     _close("out", out, ro, dtype)
     _close("h_last", h_last, rh, dtype)
     r = orc.ssm_bwd_xf(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["dout"], hp, x["dh_last"], **kw)
-    cond = {"dA": r["dA_abs"], "dD": r["dD_abs"], "ddelta_bias": r["ddelta_bias_abs"]} if conditioned else {}
+    cond = {"dA": r["dA_abs"], "dD": r["dD_abs"], "ddelta_bias": r["ddelta_bias_abs"], "ddelta": r["ddelta_abs"],
+            "du": r["du_abs"]} if conditioned else {}
     for k, name in GRADS:
         _close(name, leaves[k].grad, r[name], dtype, cond.get(name))
     if c["with_h"]:

@@ -120,34 +120,51 @@ def test_bwd_matches_autograd(shape, with_h):
         np.testing.assert_allclose(r["dh_prev"], hpl.grad.numpy(), rtol=1e-10, atol=1e-12)
 
 
+def _magnitude_sums(u, delta, A, B, C, D, hp, dout, dhl):
+    """The running-error magnitudes of dA, dΔ and du by brute force: the sequential restatement run
+    on magnitudes (|u|, |B|, |C|, |dout|, |h_prev|, |dh_last|; delta > 0 keeps |delta*u*B| =
+    delta*|u|*|B|), its state magnitudes H_t kept and its adjoint magnitudes G_t = dL+/dH_t taken from
+    torch autograd (retained gradients)."""
+    L = u.shape[1]
+    h = hp.abs().clone().requires_grad_(True)
+    hs, es, prevs = [], [], []
+    for t in range(L):
+        e = torch.exp(delta[:, t, :, None] * A[None])
+        hn = e * h + (delta[:, t] * u[:, t].abs())[..., None] * B[:, t, None, :].abs()
+        hn.retain_grad()
+        hs.append(hn), es.append(e.detach()), prevs.append(h.detach())
+        h = hn
+    out = torch.stack([(hs[t] * C[:, t, None, :].abs()).sum(-1) for t in range(L)], 1)
+    ((out * dout.abs()).sum() + (h * dhl.abs()).sum()).backward()
+    s = [es[t] * prevs[t] * hs[t].grad for t in range(L)]  # G_t dA_t H_{t-1}
+    gB = torch.stack([(B[:, t, None, :].abs() * hs[t].grad).sum(-1) for t in range(L)], 1)
+    dA = sum(delta[:, t, :, None] * s[t] for t in range(L)).sum(0)
+    dd = torch.stack([(A.abs()[None] * s[t]).sum(-1) for t in range(L)], 1) + u.abs() * gB
+    du = (D * dout).abs() + delta * gB
+    return dA, dd, du
+
+
 def test_term_magnitudes_match_autograd():
-    """dA_abs = sum_{b,t} |delta*dA_t*h_{t-1}*dL/dh_t| and dD_abs = sum_{b,t} |dout*u|, with dL/dh_t
-    taken from torch autograd (retained gradients of every state of the sequential restatement),
-    and dA_abs = dA exactly when every term is non-negative."""
+    """dA_abs, ddelta_abs, du_abs against the brute force above, dD_abs = sum_{b,t} |dout*u|; each is
+    at least its output's magnitude, above it where terms cancel, and equal to it when nothing can
+    cancel (A > 0 and u, B, C, D, dout, h_prev, dh_last >= 0)."""
     bsz, L, dm, n = 2, 13, 5, 8
     u, delta, A, B, C, D, hp = _inputs(bsz, L, dm, n, seed=61)
-    dout = torch.randn(u.shape, generator=torch.Generator().manual_seed(62), dtype=F64)
-    h = hp.clone().requires_grad_(True)
-    hs, terms = [], []
-    for t in range(L):  # the sequential recurrence with each state kept for its gradient
-        e = torch.exp(delta[:, t, :, None] * A[None])
-        hn = e * h + (delta[:, t] * u[:, t])[..., None] * B[:, t, None, :]
-        hn.retain_grad()
-        hs.append(hn)
-        terms.append((delta[:, t, :, None] * e * h).detach())
-        h = hn
-    out = torch.stack([(hs[t] * C[:, t, None, :]).sum(-1) for t in range(L)], 1) + D * u
-    (out * dout).sum().backward()
-    brute = sum((terms[t] * hs[t].grad).abs() for t in range(L)).sum(0)
-    r = orc.ssm_bwd(u, delta, A, B, C, D, dout, hp, None)
-    np.testing.assert_allclose(r["dA_abs"], brute.numpy(), rtol=1e-10, atol=1e-14)
+    g = torch.Generator().manual_seed(62)
+    dout = torch.randn(u.shape, generator=g, dtype=F64)
+    dhl = torch.randn(hp.shape, generator=g, dtype=F64)
+    r = orc.ssm_bwd(u, delta, A, B, C, D, dout, hp, dhl)
+    dA, dd, du = _magnitude_sums(u, delta, A, B, C, D, hp, dout, dhl)
+    for name, ref in (("dA_abs", dA), ("ddelta_abs", dd), ("du_abs", du)):
+        np.testing.assert_allclose(r[name], ref.numpy(), rtol=1e-10, atol=1e-14, err_msg=name)
     np.testing.assert_allclose(r["dD_abs"], (dout * u).abs().sum((0, 1)).numpy(), rtol=1e-12)
-    assert (r["dA_abs"] > np.abs(r["dA"]) + 1e-9).any()  # these terms have mixed signs
-    # all-positive terms: u, B, C, dout, h_prev >= 0 make every g, h and term >= 0
-    pos = [x.abs() for x in (u, B, C, dout, hp)]
-    r = orc.ssm_bwd(pos[0], delta, A, pos[1], pos[2], D, pos[3], pos[4], None)
-    np.testing.assert_allclose(r["dA_abs"], r["dA"], rtol=1e-12)
-    np.testing.assert_allclose(r["dD_abs"], r["dD"], rtol=1e-12)
+    for name in ("dA", "ddelta", "du", "dD"):
+        assert (r[name + "_abs"] >= np.abs(r[name]) * (1 - 1e-12)).all(), name
+        assert (r[name + "_abs"] > np.abs(r[name]) + 1e-9).any(), name  # these terms have mixed signs
+    pos = [x.abs() for x in (u, A, B, C, D, hp, dout, dhl)]
+    r = orc.ssm_bwd(pos[0], delta, pos[1], pos[2], pos[3], pos[4], pos[6], pos[5], pos[7])
+    for name in ("dA", "ddelta", "du", "dD"):
+        np.testing.assert_allclose(r[name + "_abs"], r[name], rtol=1e-12, err_msg=name)
 
 
 @pytest.mark.parametrize("bias,softplus,gate", [(True, True, True), (False, True, False), (True, False, False),
