@@ -35,17 +35,32 @@ struct SegPlan {
     int nfull = 0;
 };
 
-// A main-pass workgroup's row (b * nblk_d + channel group) and segment. Uniform plans (nfull == 0) are
-// segment-major. In a partly split plan the workgroups are nfull whole rows and two halves of each other
-// row; when the counts allow, each XCD's contiguous share of the grid (see xcd_remap) holds its whole
-// rows first and its halves after them, so that each CU receives whole rows and halves in the same
-// proportion.
+// A main-pass workgroup's row (b * nblk_d + channel group) and segment.
+// Uniform plans (nfull == 0) number the (row, segment) items segment-major, k = seg * rows + row. Each
+// XCD deals its contiguous share of the grid (see xcd_remap) to its 32 CUs breadth-first: logical
+// block j of the share runs on CU j % 32 of that XCD, as its (j / 32)-th workgroup (measured on MI355X
+// with a probe that records each workgroup's hardware CU id). When the grid is whole rounds of all 256
+// CUs, item k = round * 256 + XCD * 32 + CU, so every CU holds items from different parts of the
+// segment order: segments late in the order fold more carries before their first chunk, and a CU that
+// mixes them keeps computing while one of its workgroups folds (1-3% per call at the fill plans'
+// shapes, none at config 2). Otherwise the items follow the block order.
+// In a partly split plan the workgroups are nfull whole rows and two halves of each other row; when the
+// counts allow, each XCD's contiguous share of the grid holds its whole rows first and its halves after
+// them, so that each CU receives whole rows and halves in the same proportion.
 struct WorkItem {
     int row, seg;
     bool whole;  // the row runs unsplit in a partly split plan
 };
 __device__ __forceinline__ WorkItem main_item(int lid, int rows, int nfull, int total) {
-    if (nfull <= 0) return WorkItem{lid % rows, lid / rows, false};
+    constexpr int kXcds = 8, kCusPerXcd = 32;
+    if (nfull <= 0) {
+        int k = lid;
+        if (total % (kXcds * kCusPerXcd) == 0) {
+            const int per = total / kXcds, x = lid / per, j = lid % per;
+            k = (j / kCusPerXcd) * (kXcds * kCusPerXcd) + x * kCusPerXcd + j % kCusPerXcd;
+        }
+        return WorkItem{k % rows, k / rows, false};
+    }
     int h = lid - nfull;  // half index, or negative for a whole row
     int f = lid;
     if (nfull % 8 == 0 && total % 8 == 0) {
