@@ -22,7 +22,8 @@ case with a bias also checks the kernels' own summation: d(delta_bias) against t
 elements they output, at the elementwise bound.
 
 MWC_SWEEP_CASES=N (opt-in) adds the N cases after MWC_SWEEP_START (default 1700) of the same
-generator, under the same conditioning-aware bound for those five outputs.
+generator, and as many partly split cases (every state count), under the same conditioning-aware
+bound for those five outputs.
 """
 import os
 import random
@@ -177,3 +178,7 @@ if SWEEP_CASES > 0:  # opt-in: nothing is collected without MWC_SWEEP_CASES
     @pytest.mark.parametrize("idx", range(SWEEP_START, SWEEP_START + SWEEP_CASES))
     def test_sweep_case(dev, monkeypatch, idx):
         _run_case(dev, monkeypatch, idx, conditioned=True)
+
+    @pytest.mark.parametrize("idx", range(SWEEP_START, SWEEP_START + SWEEP_CASES))
+    def test_sweep_split_case(dev, monkeypatch, idx):
+        _run_case(dev, monkeypatch, idx, conditioned=True, c=_split_case(idx, (8, 16, 32, 64)[idx % 4]))
