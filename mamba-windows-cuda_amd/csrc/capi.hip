@@ -158,31 +158,49 @@ SegPlan plan(const SsmShape& s, bool bwd, int spl, int cap_main, int cap_carry, 
     return best;
 }
 
-// Partly split plan: when an unsplit grid leaves some CUs one workgroup short of their cap (rows between
-// (cap - 1) and cap per CU), split just enough rows into two segments that the grid fills one round:
-// x = cap * CUs - rows split rows, so a CU runs cap - 1 whole rows and one half. The halves finish at
-// half time and the CU then runs cap - 1 workgroups to the end, instead of the busiest CUs running cap
-// whole rows throughout. Only the split rows need carries. `x_forced` (MWC_NSPLIT) sets x for tests;
-// returns nseg = 0 when no such plan applies. *t_out receives the modelled time.
+// Partly split plans: only some rows are split into two segments (and need carries); the others run
+// whole. Two cases, with slots = cap * CUs workgroups in one round:
+// - rows between slots - CUs and slots (one round in which some CUs are one workgroup short of their
+//   cap): x = slots - rows split rows make the grid fill one round, each CU running cap - 1 whole rows
+//   and one half. The halves finish at half time and the CU then runs cap - 1 workgroups to the end,
+//   instead of the busiest CUs running cap whole rows throughout;
+// - rows = m full rounds plus r <= slots / 2 more (m >= 1): an unsplit grid's last round runs r whole
+//   rows on a part-empty chip. Splitting just those x = r rows puts m rounds of whole rows first (the
+//   whole rows come first in the block order) and the 2r halves in one last round of half length.
+// `x_forced` (MWC_NSPLIT) sets x for tests; returns nseg = 0 when no such plan applies. *t_out receives
+// the modelled time.
 SegPlan split_plan(const SsmShape& s, bool bwd, int spl, int cap_main, int cap_carry, double carry_rel, int x_forced,
                    double* t_out) {
     const int64_t nck = (s.seqlen + kCkptSteps - 1) / kCkptSteps;
     const int64_t rows = s.batch * ((s.dim + cpb_of(s.nstate, spl) - 1) / cpb_of(s.nstate, spl));
     const int64_t slots = (int64_t)kCUs * cap_main;
-    const int64_t x = x_forced > 0 ? x_forced : slots - rows;
+    const int64_t m = rows / slots, r = rows - m * slots;
+    const bool one_round = m == 0;
     const SegPlan none{spl, 0, 0, 0, 0};
+    int64_t x = x_forced;
+    if (x_forced <= 0) {
+        if (one_round) {
+            if (rows <= slots - kCUs || 2 * rows - slots > (int64_t)kCUs * (cap_main - 1)) return none;
+            x = slots - rows;
+        } else {
+            if (r == 0 || 2 * r > slots) return none;
+            x = r;
+        }
+    }
     if (nck < 2 || x < 1 || x >= rows) return none;
-    if (x_forced <= 0 && (rows <= slots - kCUs || 2 * rows - slots > (int64_t)kCUs * (cap_main - 1))) return none;
     for (int f = 8; f >= 1; f /= 2) {
         const int64_t cps = ((nck + 1) / 2 + f - 1) / f * f;
         const int64_t ccps = cps / f;
         if ((nck + cps - 1) / cps != 2) continue;
         if (f > 1 && (ccps < kMinSegChunks || x * f > (int64_t)kCUs * cap_carry)) continue;
         const int64_t ncar = bwd ? (nck - cps + ccps - 1) / ccps : f;
-        // a CU with cap - 1 whole rows and one half: all cap run until the half ends, then cap - 1
-        const double t = (double)cps * cap_main / simd_throughput(cap_main) +
-                         (double)(nck - cps) * (cap_main - 1) / simd_throughput(cap_main - 1) + 1.0 +
-                         carry_rel * pass_time(x * ncar, ccps, cap_carry);
+        const double carry = carry_rel * pass_time(x * ncar, ccps, cap_carry);
+        // one round: a CU with cap - 1 whole rows and one half runs all cap until the half ends, then
+        // cap - 1; several rounds: the whole rows' rounds, then the halves'
+        const double t = one_round && x == slots - rows
+                             ? (double)cps * cap_main / simd_throughput(cap_main) +
+                                   (double)(nck - cps) * (cap_main - 1) / simd_throughput(cap_main - 1) + 1.0 + carry
+                             : pass_time(rows - x, nck, cap_main) + pass_time(2 * x, cps, cap_main) + carry;
         if (t_out) *t_out = t;
         return SegPlan{spl, 2, (int)cps, f, (int)ncar, (int)(rows - x)};
     }
@@ -253,7 +271,10 @@ SegPlan plan_dir(const SsmShape& s, bool bwd) {
     const int x_forced = e ? atoi(e) : -1;  // MWC_NSPLIT=0 turns partly split plans off
     double t = 0.0, th = 0.0;
     const SegPlan p = plan(s, bwd, spl, cm, cc, rel, &t);
-    if (x_forced == 0 || (forced && x_forced < 0) || (p.nseg > 1 && x_forced < 0)) return p;
+    if (x_forced == 0 || (forced && x_forced < 0)) return p;
+    // the one-round case competes with an unsplit uniform plan only; the several-rounds case with any
+    const int64_t rows = s.batch * ((s.dim + cpb_of(s.nstate, spl) - 1) / cpb_of(s.nstate, spl));
+    if (p.nseg > 1 && x_forced < 0 && rows < (int64_t)kCUs * cm) return p;
     const SegPlan h = split_plan(s, bwd, spl, cm, cc, rel, x_forced, &th);
     return h.nseg > 0 && (x_forced > 0 || th < t * 0.98) ? h : p;
 }

@@ -168,6 +168,21 @@ def test_partly_split_nstate_case(dev, monkeypatch, n, idx):
     _run_case(dev, monkeypatch, idx, conditioned=False, c=_split_case(idx, n))
 
 
+# shapes whose grids run whole rounds of rows plus a few more: the planner's own plan splits just those
+# rows (the several-rounds partly split plan; N=64: the backward only)
+ROUNDS_CASES = (dict(B=8, L=600, D=4096, n=16, dtype=torch.float16, seed=881),
+                dict(B=8, L=300, D=1536, n=64, dtype=torch.bfloat16, seed=882))
+
+
+@pytest.mark.parametrize("idx", range(len(ROUNDS_CASES)))
+def test_planner_partly_split_rounds(dev, monkeypatch, idx):
+    c = dict(with_h=True, bias=False, softplus=False, gate=False, spl=None, nseg=None, cfold=None, lvl=0,
+             **ROUNDS_CASES[idx])
+    for var in ("MWC_SPL", "MWC_NSEG", "MWC_CFOLD", "MWC_NSPLIT"):
+        monkeypatch.delenv(var, raising=False)
+    _run_case(dev, monkeypatch, 30000 + idx, conditioned=False, c=c)
+
+
 @pytest.mark.parametrize("idx", CONDITIONED)
 def test_conditioned_case(dev, monkeypatch, idx):
     _run_case(dev, monkeypatch, idx, conditioned=True)
