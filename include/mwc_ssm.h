@@ -67,7 +67,8 @@ const char* mwc_last_error(void);
 int64_t mwc_ssm_ckpt_count(int64_t seqlen);
 
 /* Workspace bytes needed by mwc_ssm_fwd for these sizes (0 when the sequence is not split into
- * segments; otherwise the segment carries). dim is limited to 2^24. */
+ * segments; otherwise the segment carries). dim is limited to 2^24, batch*dim to 2^31 and
+ * batch*seqlen to 2^33; for sizes the entry points reject it returns 0 and sets mwc_last_error(). */
 size_t mwc_ssm_fwd_workspace_size(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate);
 
 /*
@@ -120,7 +121,8 @@ int mwc_ssm_fwd_noalloc(int dtype, const void* u, const void* delta, const void*
                         int delta_softplus, const void* z, void* out, void* out_z, void* h_last, float* ckpt,
                         int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate, void* stream);
 
-/* Workspace bytes needed by mwc_ssm_bwd for these sizes. */
+/* Workspace bytes needed by mwc_ssm_bwd for these sizes (0, with mwc_last_error() set, for sizes
+ * the entry points reject). */
 size_t mwc_ssm_bwd_workspace_size(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate);
 
 /*

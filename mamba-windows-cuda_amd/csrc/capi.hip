@@ -46,7 +46,9 @@ int check_dims(int dtype, int64_t batch, int64_t seqlen, int64_t dim, int64_t ds
     if (batch < 0 || seqlen < 0 || dim < 0)
         return fail(MWC_ERR_INVALID_ARGUMENT, "negative size (batch=%lld, seqlen=%lld, dim=%lld)", (long long)batch,
                     (long long)seqlen, (long long)dim);
-    if (seqlen > INT32_MAX / 2 || dim > (int64_t(1) << 24) || batch > 65535)
+    // the launchers count workgroups (rows of channels, rows of the dB/dC partials) in 32-bit ints
+    if (seqlen > INT32_MAX / 2 || dim > (int64_t(1) << 24) || batch > 65535 || batch * dim > (int64_t(1) << 31) ||
+        batch * seqlen > (int64_t(1) << 33))
         return fail(MWC_ERR_UNSUPPORTED, "sizes beyond the supported range (batch=%lld, seqlen=%lld, dim=%lld)",
                     (long long)batch, (long long)seqlen, (long long)dim);
     return MWC_OK;
@@ -357,11 +359,14 @@ int64_t mwc_ssm_ckpt_count(int64_t seqlen) {
     return seqlen <= 0 ? 0 : (seqlen + mwc::kCkptSteps - 1) / mwc::kCkptSteps;
 }
 
+// Sizes the entry points would reject need no workspace: 0, with the reason in mwc_last_error().
 size_t mwc_ssm_fwd_workspace_size(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate) {
+    if (check_dims(MWC_DTYPE_F32, batch, seqlen, dim, dstate) != MWC_OK) return 0;
     return mwc::fwd_workspace_bytes({batch, seqlen, dim, (int)dstate});
 }
 
 size_t mwc_ssm_bwd_workspace_size(int64_t batch, int64_t seqlen, int64_t dim, int64_t dstate) {
+    if (check_dims(MWC_DTYPE_F32, batch, seqlen, dim, dstate) != MWC_OK) return 0;
     return mwc::bwd_workspace_bytes({batch, seqlen, dim, (int)dstate});
 }
 

@@ -138,6 +138,20 @@ def test_workspace_sizes_of_empty_and_tiny_shapes():
             assert L.mwc_ssm_bwd_workspace_size(B, Lq, D, n) >= 0
 
 
+def test_workspace_sizes_of_rejected_shapes():
+    """Sizes the entry points reject (unsupported state counts, negative sizes, beyond the supported
+    range) need no workspace: the queries return 0 and name the reason, instead of planning them (a
+    state count of 4 or 0 used to divide by zero in the planner)."""
+    from mamba_windows_cuda import _lib
+
+    L = _lib.lib()
+    for B, Lq, D, n in ((2, 100, 64, 0), (2, 100, 64, 4), (2, 100, 64, 128), (-1, 100, 64, 16), (2, -5, 64, 16),
+                        (2, 100, -1, 16), (65535, 16, 1 << 24, 16), (65536, 16, 64, 16), (1 << 14, 1 << 20, 64, 16)):
+        for query in (L.mwc_ssm_fwd_workspace_size, L.mwc_ssm_bwd_workspace_size):
+            assert query(B, Lq, D, n) == 0, (B, Lq, D, n)
+            assert L.mwc_last_error(), (B, Lq, D, n)
+
+
 def test_status_strings_and_ckpt_count():
     from mamba_windows_cuda import _lib
 
